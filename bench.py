@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Benchmark: the Qwen3-30B-A3B W8 MoE layer on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--tokens T] [--copies R] [--sweep]
+
+A step is one call of the whole MoE block (router, top-k, dispatch, SwiGLU
+experts, combine) on T tokens, through the C ABI (kmoe_forward). Inputs and
+weights are resident in HBM before timing starts. To measure HBM rather than
+the 256 MB Infinity Cache, steps rotate over R independent weight copies
+(R x 604 MB) and R activation batches.
+
+Prints ONE JSON line on stdout (logs go to stderr):
+  value        decode tokens/s at T (default 64) = T*K / elapsed
+  roofline     the dominant decode kernel (gate/up + SwiGLU), HBM-bound:
+               algorithmic bytes per launch / mean launch time from HIP events
+  prefill      the 4096-token prefill chunk: tokens/s and the MFMA roofline
+               of its dominant kernel (the gate/up grouped GEMM)
+  cpu_baseline the oracle (the C restatement of the reference algorithm),
+               OpenMP on this host's cores, on a bounded sample
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+METRIC = "Qwen3-30B-A3B W8 MoE layer tokens/s; decode HBM GB/s; prefill MFMA % of peak"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Bound:
+    """One layer copy with every C struct prebuilt, so a step is one ctypes call."""
+
+    def __init__(self, layer, T, threshold=64):
+        import torch
+
+        from kappa_amd import _lib
+        from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _desc
+        from kappa_amd.qwen3.quant import weight_struct
+
+        self.layer = layer
+        dev = layer.router.device
+        self.T = T
+        self.desc = _desc(T, layer.D, layer.E, layer.K, layer.I, torch.bfloat16, threshold)
+        self.r, self._kr = weight_struct(layer.router, dev, n_out=layer.E, n_groups=None, name="router")
+        self.g, self._kg = weight_struct(layer.gate, dev, n_out=layer.I, n_groups=layer.E, name="gate")
+        self.u, self._ku = weight_struct(layer.up, dev, n_out=layer.I, n_groups=layer.E, name="up")
+        self.d, self._kd = weight_struct(layer.down, dev, n_out=layer.D, n_groups=layer.E, name="down")
+        self.packed = PACK_CACHE.get(layer.gate, layer.up, layer.down)
+        PACK_CACHE.clear()
+        self.p = self.packed.struct()
+        n = ctypes.c_size_t()
+        _lib.check(_lib.lib().kmoe_workspace_bytes(self.desc, ctypes.byref(n)))
+        self.ws = torch.empty(n.value, dtype=torch.uint8, device=dev)
+
+
+def make_copies(R, T, seed0=0):
+    from moe_cases import make_layer
+
+    return [Bound(make_layer("30b", seed=seed0 + i), T) for i in range(R)]
+
+
+def time_forward(bounds, xs, outs, steps, warmup):
+    """Whole-block steps through kmoe_forward; returns (seconds, per-step list unused)."""
+    import torch
+
+    from kappa_amd import _lib
+
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    R = len(bounds)
+
+    def step(i):
+        b = bounds[i % R]
+        st = L.kmoe_forward(
+            b.desc, xs[i % len(xs)].data_ptr(), b.r, b.g, b.u, b.d, b.p, outs[i % len(outs)].data_ptr(),
+            None, None, b.ws.data_ptr(), b.ws.numel(), stream,
+        )  # fmt: skip
+        if st:
+            _lib.check(st)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        step(warmup + i)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / 1e3
+
+
+def time_gate_up(bounds, xs, steps, decode: bool):
+    """Stage-by-stage steps with HIP events around the gate/up kernel (the dominant one).
+
+    Returns (mean gate/up ms, mean active experts U, mean rows M)."""
+    import torch
+
+    from kappa_amd.qwen3 import moe_stages
+
+    ev = []
+    actives = []
+    for i in range(steps):
+        b = bounds[i % len(bounds)]
+        lay = b.layer
+        x = xs[i % len(xs)]
+        r = moe_stages.route(x, lay.router, num_experts=lay.E, k=lay.K)
+        dsp = moe_stages.dispatch(r["idx"], r["hist"], num_experts=lay.E)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        h, y = _gate_up_only(b, x, dsp, decode)
+        e1.record()
+        ev.append((e0, e1))
+        actives.append(dsp["active"][lay.E : lay.E + 1])
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(c) for a, c in ev]
+    U = float(torch.cat(actives).float().mean().item())
+    return statistics.mean(ms[1:] if len(ms) > 2 else ms), U, ms
+
+
+def _gate_up_only(b, x, dsp, decode):
+    import torch
+
+    from kappa_amd import _lib
+
+    lay = b.layer
+    T = x.shape[0]
+    h = torch.empty((T * lay.K, lay.I), dtype=torch.bfloat16, device=x.device)
+    desc = type(b.desc)(T, lay.D, lay.E, lay.K, lay.I, 1, 64 if decode else 0)
+    _lib.check(
+        _lib.lib().kmoe_expert_gate_up(
+            desc, x.data_ptr(), dsp["offsets"].data_ptr(), dsp["active"].data_ptr(), dsp["sorted_token"].data_ptr(),
+            dsp["sorted_expert"].data_ptr(), b.g, b.u, b.p, h.data_ptr(), torch.cuda.current_stream().cuda_stream,
+        )
+    )  # fmt: skip
+    return h, None
+
+
+def cpu_baseline(layer, T, budget_s=12.0, max_reps=20):
+    """Time the oracle (C, OpenMP) on the same workload; bounded sample."""
+    import numpy as np
+
+    import oracle
+
+    host = layer.host()
+    x = layer_x_host(T, layer.D)
+    threads = len(os.sched_getaffinity(0))
+    oracle.set_threads(threads)
+    oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True)  # warm
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    cpu = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": T / med,
+        "unit": "tokens/s",
+        "cores": oracle.get_threads(),
+        "kind": "port",
+        "sample": f"{len(times)} full layer calls at T={T} (30B-A3B W8, bf16), median {med * 1e3:.1f} ms; CPU: {cpu}",
+    }
+
+
+def layer_x_host(T, D, seed=99):
+    import numpy as np
+
+    from inputs import bf16_rne
+
+    rng = np.random.default_rng(seed)
+    return bf16_rne(rng.standard_normal((T, D)).astype(np.float32))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--tokens", type=int, default=64)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--prefill-tokens", type=int, default=4096)
+    ap.add_argument("--sweep", action="store_true", help="also time decode T in {1, 8, 32}")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the MoE block is not "
+            "sharded across GPUs",
+            file=sys.stderr,
+        )
+        sys.exit(1)
+
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import torch
+
+    from kappa_amd import _lib
+
+    _lib.lib()
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T = args.tokens
+    R = args.copies
+    log(f"bench: building {R} weight copies of the 30B-A3B W8 layer")
+    bounds = make_copies(R, T)
+    lay0 = bounds[0].layer
+    D, E, K, I = lay0.D, lay0.E, lay0.K, lay0.I
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    xs = [torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(R)]
+    outs = [torch.empty(T, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+
+    log(f"bench: decode T={T}: {args.warmup} warmup + {args.steps} timed steps")
+    secs = time_forward(bounds, xs, outs, args.steps, args.warmup)
+    ms_step = secs * 1e3 / args.steps
+    tok_s = T * args.steps / secs
+    log(f"bench: decode T={T}: {ms_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s")
+
+    gu_ms, U, _ = time_gate_up(bounds, xs, max(args.steps, 16), decode=True)
+    M = T * K
+    gu_bytes = U * (2 * D * I + 2 * I * 4) + T * D * 2 + M * I * 2
+    gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
+    layer_bytes = U * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 2 * (2 * T * D)
+    log(f"bench: gate/up kernel {gu_ms * 1e3:.1f} us, U={U:.1f}, {gu_gbs:.0f} GB/s")
+    result = {
+        "metric": METRIC,
+        "value": tok_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"qwen3-30b-a3b W8 MoE layer, decode batch T={T}",
+            "tokens": T,
+            "hidden": D,
+            "experts": E,
+            "top_k": K,
+            "intermediate": I,
+            "weights": "int8 per-output-channel fp32 scales, quantised from N(0,0.02)",
+            "weight_copies_rotated": R,
+        },
+        "roofline": {
+            "kernel": "k_gateup_decode",
+            "bound": "hbm",
+            "achieved": gu_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": gu_gbs / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes_per_launch": gu_bytes,
+            "mean_launch_us": gu_ms * 1e3,
+            "active_experts": U,
+        },
+        "layer_hbm_gbs": layer_bytes / (ms_step * 1e-3) / 1e9,
+    }
+    result["layer_hbm_frac"] = result["layer_hbm_gbs"] / HBM_PEAK_GBS
+
+    if args.sweep:
+        sweep = {}
+        for Ts in (1, 8, 32):
+            bs = [Bound(b.layer, Ts) for b in bounds]
+            xs_s = [x[:Ts].contiguous() for x in xs]
+            o_s = [torch.empty(Ts, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+            s = time_forward(bs, xs_s, o_s, args.steps, args.warmup)
+            gms, Us, _ = time_gate_up(bs, xs_s, max(args.steps, 16), decode=True)
+            gb = Us * (2 * D * I + 2 * I * 4) + Ts * D * 2 + Ts * K * I * 2
+            lb = Us * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 2 * (2 * Ts * D)
+            sweep[str(Ts)] = {
+                "tokens_per_s": Ts * args.steps / s,
+                "us_per_step": s * 1e6 / args.steps,
+                "layer_hbm_gbs": lb / (s / args.steps) / 1e9,
+                "gate_up_us": gms * 1e3,
+                "gate_up_gbs": gb / (gms * 1e-3) / 1e9,
+                "active_experts": Us,
+            }
+            log(f"bench: decode T={Ts}: {sweep[str(Ts)]}")
+        result["decode_sweep"] = sweep
+
+    if not args.no_prefill:
+        Tp = args.prefill_tokens
+        log(f"bench: prefill T={Tp}")
+        bp = [Bound(b.layer, Tp) for b in bounds[:2]]
+        gp = torch.Generator(device=dev)
+        gp.manual_seed(11)
+        xp = [torch.randn(Tp, D, generator=gp, device=dev).to(torch.bfloat16) for _ in range(2)]
+        op = [torch.empty(Tp, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+        psteps = max(10, args.steps // 5)
+        s = time_forward(bp, xp, op, psteps, 3)
+        gms, Up, _ = time_gate_up(bp, xp, psteps, decode=False)
+        Mp = Tp * K
+        flops_gu = 2.0 * Mp * D * 2 * I
+        flops_layer = 2.0 * Tp * K * 3 * D * I + 2.0 * Tp * D * E
+        tf = flops_gu / (gms * 1e-3) / 1e12
+        result["prefill"] = {
+            "workload": f"qwen3-30b-a3b W8 MoE layer, prefill chunk T={Tp}",
+            "tokens_per_s": Tp * psteps / s,
+            "ms_per_step": s * 1e3 / psteps,
+            "layer_tflops": flops_layer / (s / psteps) / 1e12,
+            "layer_mfma_frac": flops_layer / (s / psteps) / 1e12 / BF16_PEAK_TFLOPS,
+            "roofline": {
+                "kernel": "k_prefill<true> (gate/up grouped GEMM + SwiGLU)",
+                "bound": "mfma",
+                "achieved": tf,
+                "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": tf / BF16_PEAK_TFLOPS,
+                "traffic": None,
+                "algorithmic_flops_per_launch": flops_gu,
+                "mean_launch_us": gms * 1e3,
+            },
+        }
+        log(f"bench: prefill {result['prefill']}")
+
+    if not args.no_cpu_baseline:
+        log("bench: CPU baseline (oracle)")
+        result["cpu_baseline"] = cpu_baseline(bounds[0].layer, T)
+        log(f"bench: cpu {result['cpu_baseline']}")
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

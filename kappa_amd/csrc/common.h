@@ -1,0 +1,78 @@
+// Shared device helpers for the gfx950 MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kmoe.h"
+
+namespace kmoe {
+
+// Slice length of the canonical router summation order: each slice of 64
+// consecutive hidden indices is a sequential fmaf chain from +0.0f, and the
+// slice partials are combined by a pairwise tree.
+constexpr int kRouterSlice = 64;
+// Tokens per dispatch block (per-block expert histograms).
+constexpr int kDispatchBlock = 64;
+// Largest expert count / top-k the routing kernels hold in registers and LDS.
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopK = 64;
+constexpr int kMaxRouterSlices = 64;  // D <= 4096
+// Decode kernels keep up to this many 16-row blocks of one expert in registers.
+constexpr int kDecodeMaxRowBlocks = 4;  // T <= 64 tokens
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Round-to-nearest-even float -> bf16 bits (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// Activation element access, templated on storage type (uint16_t = bf16 bits, float = f32).
+template <typename A>
+struct Act;
+template <>
+struct Act<float> {
+  static constexpr bool kBf16 = false;
+  __device__ __forceinline__ static float load(const float* p, int64_t i) { return p[i]; }
+  __device__ __forceinline__ static float round(float v) { return v; }
+  __device__ __forceinline__ static void store(float* p, int64_t i, float v) { p[i] = v; }
+};
+template <>
+struct Act<uint16_t> {
+  static constexpr bool kBf16 = true;
+  __device__ __forceinline__ static float load(const uint16_t* p, int64_t i) { return bf16_bits_to_f32(p[i]); }
+  __device__ __forceinline__ static float round(float v) { return round_bf16(v); }
+  __device__ __forceinline__ static void store(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16_bits(v); }
+};
+
+// silu(g) = g / (1 + exp(-g)) (jax.nn.silu, kappa/qwen3/ffn_moe.py:101)
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace kmoe
+
+// Host-side helpers shared by the launch wrappers.
+namespace kmoe_host {
+
+inline size_t dtype_size(kmoe_dtype t) {
+  switch (t) {
+    case KMOE_DTYPE_F32:
+      return 4;
+    case KMOE_DTYPE_BF16:
+      return 2;
+    case KMOE_DTYPE_I8:
+      return 1;
+  }
+  return 0;
+}
+
+}  // namespace kmoe_host

@@ -1,0 +1,647 @@
+// SwiGLU experts over the dispatch-sorted rows, and the weighted combine.
+//
+// Reference: _moe_gather_einsum (kappa/qwen3/ffn_moe.py:74-104) for the
+// rounding points, _moe_ragged (kappa/qwen3/ffn_moe.py:174-216) for the
+// grouped form: every expert's weights are read once per row tile instead of
+// once per assignment.
+//
+// Packed int8 experts (bf16 activations) run on bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16); int8 is dequantised in registers to
+// bf16(q * bf16(scale)) right after a coalesced 16-byte load. The MFMA k order
+// inside a 64-wide chunk is permuted: lane l supplies k = 16*(l/16) + 8*s + 0..7
+// in sub-step s, for both operands, which matches the packed layout
+// [.., k/16, col, 16 k] where each lane's 16 bytes are one column's 16 k.
+#include "common.h"
+#include "launch.h"
+
+namespace kmoe {
+
+// ---------------------------------------------------------------------------
+// helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void dequant16(const uint4 q, const float s, bf16x8& lo, bf16x8& hi) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int8_t b = (int8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
+    lo[j] = (__bf16)((float)b * s);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int8_t b = (int8_t)((w[2 + (j >> 2)] >> (8 * (j & 3))) & 0xffu);
+    hi[j] = (__bf16)((float)b * s);
+  }
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ floatx4 mfma16(const bf16x8 a, const bf16x8 b, const floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Block-wide tile prefix over experts: mtp[e] = sum_{e' < e} ceil(group_size[e'] / BM), mtp[E] = total.
+// blockDim.x must be 256.
+template <int BM>
+__device__ void tile_prefix(const int32_t* __restrict__ offsets, int E, int* mtp) {
+  __shared__ int wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  int c[4];
+  int local = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid * 4 + i;
+    c[i] = 0;
+    if (e < E) c[i] = (offsets[e + 1] - offsets[e] + BM - 1) / BM;
+    local += c[i];
+  }
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
+  }
+  if (lane == 63) wsum[wv] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wv; ++w) base += wsum[w];
+  int run = base + incl - local;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid * 4 + i;
+    if (e < E) mtp[e] = run;
+    run += c[i];
+  }
+  if (tid == 255) mtp[E] = base + incl;
+  __syncthreads();
+}
+
+// largest e in [0, E) with mtp[e] <= v (mtp non-decreasing, mtp[0] = 0)
+__device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (mtp[mid] <= v)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+// ---------------------------------------------------------------------------
+// Decode (T <= 64): one block per (active expert, 16-column group); the four
+// waves split the reduction axis and are summed in wave order through LDS.
+// Each weight byte is read exactly once per call.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_gateup_decode(int D, int I, int E, const uint16_t* __restrict__ x,
+                                                        const int32_t* __restrict__ offsets,
+                                                        const int32_t* __restrict__ active,
+                                                        const int32_t* __restrict__ sorted_token,
+                                                        const int8_t* __restrict__ w13, const float* __restrict__ s13,
+                                                        uint16_t* __restrict__ h_sorted) {
+  __shared__ floatx4 red[3][kDecodeMaxRowBlocks][2][64];
+  const int ig = blockIdx.x;
+  const int slot = blockIdx.y;
+  if (slot >= active[E]) return;
+  const int e = active[slot];
+  const int r0 = offsets[e];
+  const int nrows = offsets[e + 1] - r0;
+  const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int IG = I >> 4, KC = D >> 6;
+  const size_t cell = (size_t)(D >> 4) * 256;
+  const int8_t* bg = w13 + (((size_t)e * IG + ig) * 2 + 0) * cell;
+  const int8_t* bu = bg + cell;
+  const float sg = s13[(((size_t)e * IG + ig) * 2 + 0) * 16 + (lane & 15)];
+  const float su = s13[(((size_t)e * IG + ig) * 2 + 1) * 16 + (lane & 15)];
+  int tok[kDecodeMaxRowBlocks];
+#pragma unroll
+  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+    const int row = rb * 16 + (lane & 15);
+    tok[rb] = (rb < nrb && row < nrows) ? sorted_token[r0 + row] : -1;
+  }
+  floatx4 ag[kDecodeMaxRowBlocks], au[kDecodeMaxRowBlocks];
+#pragma unroll
+  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+    ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  const int c0 = (KC * wv) >> 2, c1 = (KC * (wv + 1)) >> 2;
+  const int koff = 16 * (lane >> 4);
+  for (int c = c0; c < c1; ++c) {
+    const uint4 qg = *reinterpret_cast<const uint4*>(bg + (size_t)c * 1024 + lane * 16);
+    const uint4 qu = *reinterpret_cast<const uint4*>(bu + (size_t)c * 1024 + lane * 16);
+    bf16x8 bg0, bg1, bu0, bu1;
+    dequant16(qg, sg, bg0, bg1);
+    dequant16(qu, su, bu0, bu1);
+#pragma unroll
+    for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+      if (rb < nrb) {
+        uint4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+        if (tok[rb] >= 0) {
+          const uint4* ap = reinterpret_cast<const uint4*>(x + (size_t)tok[rb] * D + c * 64 + koff);
+          a0 = ap[0];
+          a1 = ap[1];
+        }
+        ag[rb] = mfma16(as_bf16x8(a0), bg0, ag[rb]);
+        ag[rb] = mfma16(as_bf16x8(a1), bg1, ag[rb]);
+        au[rb] = mfma16(as_bf16x8(a0), bu0, au[rb]);
+        au[rb] = mfma16(as_bf16x8(a1), bu1, au[rb]);
+      }
+    }
+  }
+  if (wv > 0) {
+#pragma unroll
+    for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+      red[wv - 1][rb][0][lane] = ag[rb];
+      red[wv - 1][rb][1][lane] = au[rb];
+    }
+  }
+  __syncthreads();
+  if (wv != 0) return;
+#pragma unroll
+  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+    if (rb >= nrb) break;
+    floatx4 g = ag[rb], u = au[rb];
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+      g += red[w][rb][0][lane];
+      u += red[w][rb][1][lane];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = rb * 16 + 4 * (lane >> 4) + j;
+      if (row < nrows) {
+        const float gv = round_bf16(g[j]), uv = round_bf16(u[j]);
+        h_sorted[(size_t)(r0 + row) * I + ig * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(gv) * uv);
+      }
+    }
+  }
+}
+
+template <int NCG>
+__global__ __launch_bounds__(256) void k_down_decode(int D, int I, int E, const uint16_t* __restrict__ h_sorted,
+                                                      const int32_t* __restrict__ offsets,
+                                                      const int32_t* __restrict__ active,
+                                                      const int8_t* __restrict__ w2, const float* __restrict__ s2,
+                                                      uint16_t* __restrict__ y_sorted) {
+  __shared__ floatx4 red[3][kDecodeMaxRowBlocks][NCG][64];
+  const int dt = blockIdx.x;  // NCG*16 output columns
+  const int slot = blockIdx.y;
+  if (slot >= active[E]) return;
+  const int e = active[slot];
+  const int r0 = offsets[e];
+  const int nrows = offsets[e + 1] - r0;
+  const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int DG = D >> 4, KC = I >> 6;
+  const size_t cell = (size_t)(I >> 4) * 256;
+  float sc[NCG];
+  const int8_t* bp[NCG];
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) {
+    const int dg = dt * NCG + cg;
+    bp[cg] = w2 + ((size_t)e * DG + dg) * cell;
+    sc[cg] = s2[(size_t)e * D + dg * 16 + (lane & 15)];
+  }
+  floatx4 acc[kDecodeMaxRowBlocks][NCG];
+#pragma unroll
+  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb)
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) acc[rb][cg] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int c0 = (KC * wv) >> 2, c1 = (KC * (wv + 1)) >> 2;
+  const int koff = 16 * (lane >> 4);
+  for (int c = c0; c < c1; ++c) {
+    bf16x8 b0[NCG], b1[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const uint4 q = *reinterpret_cast<const uint4*>(bp[cg] + (size_t)c * 1024 + lane * 16);
+      dequant16(q, sc[cg], b0[cg], b1[cg]);
+    }
+#pragma unroll
+    for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+      if (rb < nrb) {
+        const int row = rb * 16 + (lane & 15);
+        uint4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+        if (row < nrows) {
+          const uint4* ap = reinterpret_cast<const uint4*>(h_sorted + (size_t)(r0 + row) * I + c * 64 + koff);
+          a0 = ap[0];
+          a1 = ap[1];
+        }
+#pragma unroll
+        for (int cg = 0; cg < NCG; ++cg) {
+          acc[rb][cg] = mfma16(as_bf16x8(a0), b0[cg], acc[rb][cg]);
+          acc[rb][cg] = mfma16(as_bf16x8(a1), b1[cg], acc[rb][cg]);
+        }
+      }
+    }
+  }
+  if (wv > 0) {
+#pragma unroll
+    for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb)
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) red[wv - 1][rb][cg][lane] = acc[rb][cg];
+  }
+  __syncthreads();
+  if (wv != 0) return;
+#pragma unroll
+  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+    if (rb >= nrb) break;
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      floatx4 v = acc[rb][cg];
+#pragma unroll
+      for (int w = 0; w < 3; ++w) v += red[w][rb][cg][lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = rb * 16 + 4 * (lane >> 4) + j;
+        if (row < nrows)
+          y_sorted[(size_t)(r0 + row) * D + (dt * NCG + cg) * 16 + (lane & 15)] = f32_to_bf16_bits(v[j]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill: grouped GEMM over (expert, 128-row tile, column tile) work items.
+// 4 waves as 2 (rows) x 2 (columns); each wave owns 64 rows. A (activation
+// rows) and B (dequantised weights) are staged in double-buffered LDS in
+// 64-deep k chunks; one barrier per chunk. Work items are laid out so that all
+// column tiles of one (expert, row tile) run on the same XCD (its L2).
+// ---------------------------------------------------------------------------
+constexpr int kBM = 128;
+constexpr int kAStride = 72;  // bf16 elements per LDS row (64 + 8 pad: conflict-free fragment reads)
+
+struct PrefillLds {
+  uint16_t a[2][kBM][kAStride];
+  uint16_t b[2][2][8][64][8];  // [buf][sub-step][col group][lane][8 bf16]
+  int mtp[kMaxExperts + 1];
+  int tok[kBM];
+};
+
+__device__ __forceinline__ bool prefill_tile(const int32_t* __restrict__ offsets, int E, int NT, PrefillLds& s,
+                                             int& e, int& row0, int& rows, int& nt) {
+  tile_prefix<kBM>(offsets, E, s.mtp);
+  const int ntiles = s.mtp[E] * NT;
+  const int per = (ntiles + 7) >> 3;
+  const int q = blockIdx.x >> 3;
+  if (q >= per) return false;
+  const int L = (blockIdx.x & 7) * per + q;
+  if (L >= ntiles) return false;
+  const int mt_glob = L / NT;
+  nt = L - mt_glob * NT;
+  e = tile_expert(s.mtp, E, mt_glob);
+  const int mt = mt_glob - s.mtp[e];
+  row0 = offsets[e] + mt * kBM;
+  rows = min(kBM, offsets[e + 1] - row0);
+  return true;
+}
+
+// GATEUP = true: A rows gathered from x by token, B = gate|up column groups,
+// epilogue SwiGLU -> h_sorted. GATEUP = false: A = h_sorted rows, B = down,
+// epilogue -> y_sorted.
+template <bool GATEUP>
+__global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const uint16_t* __restrict__ src,
+                                                     const int32_t* __restrict__ offsets,
+                                                     const int32_t* __restrict__ sorted_token,
+                                                     const int8_t* __restrict__ wp, const float* __restrict__ sp,
+                                                     uint16_t* __restrict__ dst) {
+  __shared__ PrefillLds s;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int Kdim = GATEUP ? D : I;
+  const int Ndim = GATEUP ? I : D;
+  const int NT = GATEUP ? (I >> 6) : (D >> 7);
+  int e, row0, rows, nt;
+  if (!prefill_tile(offsets, E, NT, s, e, row0, rows, nt)) return;
+  if (tid < kBM) s.tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
+  __syncthreads();
+
+  // global -> LDS mapping
+  const int ar = tid >> 1, ah = tid & 1;
+  const int arow = s.tok[ar];
+  const uint16_t* ap = arow >= 0 ? src + (size_t)arow * Kdim + ah * 32 : nullptr;
+  const int cg = tid >> 5;
+  const int l0 = (tid & 31) << 1;
+  const int8_t* bp;
+  float sc0, sc1;
+  if (GATEUP) {
+    const int which = cg >> 2;
+    const int igl = nt * 4 + (cg & 3);
+    const size_t cid = ((size_t)e * (I >> 4) + igl) * 2 + which;
+    bp = wp + cid * (size_t)(D >> 4) * 256;
+    sc0 = sp[cid * 16 + (l0 & 15)];
+    sc1 = sp[cid * 16 + ((l0 + 1) & 15)];
+  } else {
+    const int dg = nt * 8 + cg;
+    bp = wp + ((size_t)e * (D >> 4) + dg) * (size_t)(I >> 4) * 256;
+    sc0 = sp[(size_t)e * D + dg * 16 + (l0 & 15)];
+    sc1 = sp[(size_t)e * D + dg * 16 + ((l0 + 1) & 15)];
+  }
+
+  uint4 ra[4], rq[2];
+  auto gload = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ra[j] = ap ? reinterpret_cast<const uint4*>(ap + c * 64)[j] : uint4{0, 0, 0, 0};
+    rq[0] = *reinterpret_cast<const uint4*>(bp + (size_t)c * 1024 + l0 * 16);
+    rq[1] = *reinterpret_cast<const uint4*>(bp + (size_t)c * 1024 + (l0 + 1) * 16);
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(&s.a[buf][ar][ah * 32 + 8 * j]) = ra[j];
+    bf16x8 lo, hi;
+    dequant16(rq[0], sc0, lo, hi);
+    *reinterpret_cast<bf16x8*>(&s.b[buf][0][cg][l0][0]) = lo;
+    *reinterpret_cast<bf16x8*>(&s.b[buf][1][cg][l0][0]) = hi;
+    dequant16(rq[1], sc1, lo, hi);
+    *reinterpret_cast<bf16x8*>(&s.b[buf][0][cg][l0 + 1][0]) = lo;
+    *reinterpret_cast<bf16x8*>(&s.b[buf][1][cg][l0 + 1][0]) = hi;
+  };
+
+  const int wm = wv & 1, wn = wv >> 1;
+  // accumulators: GATEUP: [mi][ni 0..1][gate/up]; down: [mi][ni 0..3]
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[mi][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // column groups of this wave, in acc order
+  int wcg[4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n) wcg[n] = GATEUP ? ((n & 1) ? 4 : 0) + wn * 2 + (n >> 1) : wn * 4 + n;
+  int mlim = 0;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+    if (wm * 64 + mi * 16 < rows) mlim = mi + 1;
+
+  const int KC = Kdim >> 6;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int c = 0; c < KC; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < KC) gload(c + 1);
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      bf16x8 a[4], b[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        a[mi] = *reinterpret_cast<const bf16x8*>(&s.a[buf][wm * 64 + mi * 16 + (lane & 15)][16 * (lane >> 4) + 8 * st]);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) b[n] = *reinterpret_cast<const bf16x8*>(&s.b[buf][st][wcg[n]][lane][0]);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        if (mi < mlim) {
+#pragma unroll
+          for (int n = 0; n < 4; ++n) acc[mi][n] = mfma16(a[mi], b[n], acc[mi][n]);
+        }
+      }
+    }
+    if (c + 1 < KC) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 4*(lane/16)+j of each 16x16 tile, column lane%16
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = wm * 64 + mi * 16 + 4 * (lane >> 4) + j;
+      if (row >= rows) continue;
+      uint16_t* drow = dst + (size_t)(row0 + row) * Ndim;
+      if (GATEUP) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) {
+          const float g = round_bf16(acc[mi][2 * ni][j]);
+          const float u = round_bf16(acc[mi][2 * ni + 1][j]);
+          drow[nt * 64 + wn * 32 + ni * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(g) * u);
+        }
+      } else {
+#pragma unroll
+        for (int n = 0; n < 4; ++n) drow[nt * 128 + wn * 64 + n * 16 + (lane & 15)] = f32_to_bf16_bits(acc[mi][n][j]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Layout-native experts: one thread per output element, a sequential fmaf
+// chain over the reduction axis from +0.0f (the oracle's order). Serves the
+// f32 configuration, plain-weight layers and unpacked int8 weights.
+// ---------------------------------------------------------------------------
+struct WView {
+  const void* v;
+  const void* s;
+  int wt;  // 0 f32, 1 bf16, 2 int8
+  int s_bf16;
+  int per_channel;
+};
+
+template <bool BF16>
+__device__ __forceinline__ float w_at(const WView& w, size_t idx, size_t sidx) {
+  if (w.wt == 0) {
+    const float v = reinterpret_cast<const float*>(w.v)[idx];
+    return BF16 ? round_bf16(v) : v;
+  }
+  if (w.wt == 1) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(w.v)[idx]);
+  const float q = (float)reinterpret_cast<const int8_t*>(w.v)[idx];
+  const size_t si = w.per_channel ? sidx : 0;
+  const float sv = w.s_bf16 ? bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(w.s)[si])
+                            : reinterpret_cast<const float*>(w.s)[si];
+  return BF16 ? round_bf16(q * round_bf16(sv)) : q * sv;
+}
+
+template <typename A>
+__global__ __launch_bounds__(256) void k_gateup_generic(int D, int I, const A* __restrict__ x,
+                                                         const int32_t* __restrict__ sorted_token,
+                                                         const int32_t* __restrict__ sorted_expert, WView wg, WView wu,
+                                                         A* __restrict__ h_sorted) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y;
+  if (i >= I) return;
+  const int t = sorted_token[m], e = sorted_expert[m];
+  float g = 0.0f, u = 0.0f;
+  for (int d = 0; d < D; ++d) {
+    const float xv = Act<A>::load(x, (int64_t)t * D + d);
+    const size_t idx = ((size_t)e * D + d) * I + i;
+    g = __builtin_fmaf(xv, w_at<Act<A>::kBf16>(wg, idx, (size_t)e * I + i), g);
+    u = __builtin_fmaf(xv, w_at<Act<A>::kBf16>(wu, idx, (size_t)e * I + i), u);
+  }
+  g = Act<A>::round(g);
+  u = Act<A>::round(u);
+  Act<A>::store(h_sorted, (int64_t)m * I + i, silu_f32(g) * u);
+}
+
+template <typename A>
+__global__ __launch_bounds__(256) void k_down_generic(int D, int I, const A* __restrict__ h_sorted,
+                                                       const int32_t* __restrict__ sorted_expert, WView wd,
+                                                       A* __restrict__ y_sorted) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int m = blockIdx.y;
+  if (n >= D) return;
+  const int e = sorted_expert[m];
+  float acc = 0.0f;
+  for (int i = 0; i < I; ++i) {
+    const float hv = Act<A>::load(h_sorted, (int64_t)m * I + i);
+    acc = __builtin_fmaf(hv, w_at<Act<A>::kBf16>(wd, ((size_t)e * I + i) * D + n, (size_t)e * D + n), acc);
+  }
+  Act<A>::store(y_sorted, (int64_t)m * D + n, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Combine: out[t, n] = round(sum_{j<K} w[t,j] * y_sorted[inv[t*K+j], n]),
+// sequential fmaf over j from +0.0f; no atomics, one writer per element.
+// ---------------------------------------------------------------------------
+template <typename A, int VEC>
+__global__ __launch_bounds__(256) void k_combine(int T, int K, int D, const A* __restrict__ y,
+                                                  const int32_t* __restrict__ inv, const float* __restrict__ w,
+                                                  A* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int n0 = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+  if (n0 >= D) return;
+  float acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+  for (int j = 0; j < K; ++j) {
+    const float wj = w[(int64_t)t * K + j];
+    const A* yr = y + (int64_t)inv[(int64_t)t * K + j] * D;
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+      if (VEC == 1 || n0 + v < D) acc[v] = __builtin_fmaf(wj, Act<A>::load(yr, n0 + v), acc[v]);
+  }
+#pragma unroll
+  for (int v = 0; v < VEC; ++v)
+    if (VEC == 1 || n0 + v < D) Act<A>::store(out, (int64_t)t * D + n0 + v, acc[v]);
+}
+
+template <typename A>
+__global__ __launch_bounds__(256) void k_cast_from_f32(int64_t n, const float* __restrict__ in, A* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) Act<A>::store(out, i, in[i]);
+}
+
+}  // namespace kmoe
+
+namespace kmoe_host {
+
+using namespace kmoe;
+
+hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, const void* x, const int32_t* offsets,
+                                const int32_t* active, const int32_t* sorted_token, const kmoe_packed_experts& p,
+                                void* h_sorted, void* y_sorted, hipStream_t st) {
+  const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts, K = (int)d.top_k,
+            I = (int)d.intermediate;
+  const int M = T * K;
+  const int slots = M < E ? M : E;
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(x);
+  uint16_t* hb = reinterpret_cast<uint16_t*>(h_sorted);
+  uint16_t* yb = reinterpret_cast<uint16_t*>(y_sorted);
+  const int8_t* w13 = reinterpret_cast<const int8_t*>(p.w13);
+  const int8_t* w2 = reinterpret_cast<const int8_t*>(p.w2);
+  const float* s13 = reinterpret_cast<const float*>(p.s13);
+  const float* s2 = reinterpret_cast<const float*>(p.s2);
+  if (decode) {
+    if (stages & kStageGateUp) {
+      hipLaunchKernelGGL(k_gateup_decode, dim3(I / 16, slots), dim3(256), 0, st, D, I, E, xb, offsets, active,
+                         sorted_token, w13, s13, hb);
+      hipError_t err = hipGetLastError();
+      if (err != hipSuccess) return err;
+    }
+    if (stages & kStageDown) {
+      hipLaunchKernelGGL((k_down_decode<2>), dim3(D / 32, slots), dim3(256), 0, st, D, I, E, hb, offsets, active,
+                         w2, s2, yb);
+      return hipGetLastError();
+    }
+    return hipSuccess;
+  }
+  const int upper_mt = (M + kBM - 1) / kBM + slots;
+  auto grid_for = [&](int NT) {
+    int g = upper_mt * NT;
+    return ((g + 7) / 8) * 8;
+  };
+  if (stages & kStageGateUp) {
+    hipLaunchKernelGGL((k_prefill<true>), dim3(grid_for(I / 64)), dim3(256), 0, st, D, I, E, xb, offsets,
+                       sorted_token, w13, s13, hb);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (stages & kStageDown) {
+    hipLaunchKernelGGL((k_prefill<false>), dim3(grid_for(D / 128)), dim3(256), 0, st, D, I, E, hb, offsets,
+                       sorted_token, w2, s2, yb);
+    return hipGetLastError();
+  }
+  return hipSuccess;
+}
+
+static WView make_view(const kmoe_weight& w) {
+  WView v;
+  v.v = w.values;
+  v.s = w.scale;
+  v.wt = w.dtype == KMOE_DTYPE_F32 ? 0 : (w.dtype == KMOE_DTYPE_BF16 ? 1 : 2);
+  v.s_bf16 = (w.dtype == KMOE_DTYPE_I8 && w.scale_dtype == KMOE_DTYPE_BF16) ? 1 : 0;
+  v.per_channel = (w.dtype == KMOE_DTYPE_I8 && w.scale_kind == KMOE_SCALE_CHANNEL) ? 1 : 0;
+  return v;
+}
+
+template <typename A>
+static hipError_t generic_stages(int stages, int D, int I, int M, const void* x, const int32_t* sorted_token,
+                                 const int32_t* sorted_expert, const WView& wg, const WView& wu, const WView& wd,
+                                 void* h_sorted, void* y_sorted, hipStream_t st) {
+  if (stages & kStageGateUp) {
+    hipLaunchKernelGGL((k_gateup_generic<A>), dim3((I + 255) / 256, M), dim3(256), 0, st, D, I,
+                       reinterpret_cast<const A*>(x), sorted_token, sorted_expert, wg, wu,
+                       reinterpret_cast<A*>(h_sorted));
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (stages & kStageDown) {
+    hipLaunchKernelGGL((k_down_generic<A>), dim3((D + 255) / 256, M), dim3(256), 0, st, D, I,
+                       reinterpret_cast<const A*>(h_sorted), sorted_expert, wd, reinterpret_cast<A*>(y_sorted));
+    return hipGetLastError();
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, const int32_t* sorted_token,
+                                 const int32_t* sorted_expert, const kmoe_weight* gate, const kmoe_weight* up,
+                                 const kmoe_weight* down, void* h_sorted, void* y_sorted, hipStream_t st) {
+  const int T = (int)d.tokens, D = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
+  const int M = T * K;
+  const WView none = {nullptr, nullptr, 0, 0, 0};
+  const WView wg = gate ? make_view(*gate) : none, wu = up ? make_view(*up) : none,
+              wd = down ? make_view(*down) : none;
+  if (d.act_dtype == KMOE_DTYPE_BF16)
+    return generic_stages<uint16_t>(stages, D, I, M, x, sorted_token, sorted_expert, wg, wu, wd, h_sorted, y_sorted,
+                                    st);
+  return generic_stages<float>(stages, D, I, M, x, sorted_token, sorted_expert, wg, wu, wd, h_sorted, y_sorted, st);
+}
+
+hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
+                          hipStream_t st) {
+  const int T = (int)d.tokens, D = (int)d.hidden, K = (int)d.top_k;
+  if (d.act_dtype == KMOE_DTYPE_BF16) {
+    if (D % 8 == 0)
+      hipLaunchKernelGGL((k_combine<uint16_t, 8>), dim3((D / 8 + 255) / 256, T), dim3(256), 0, st, T, K, D,
+                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out));
+    else
+      hipLaunchKernelGGL((k_combine<uint16_t, 1>), dim3((D + 255) / 256, T), dim3(256), 0, st, T, K, D,
+                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out));
+  } else {
+    hipLaunchKernelGGL((k_combine<float, 1>), dim3((D + 255) / 256, T), dim3(256), 0, st, T, K, D,
+                       reinterpret_cast<const float*>(y_sorted), inv, topk_w, reinterpret_cast<float*>(out));
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_topk_w_cast(const kmoe_desc& d, const float* topk_w, void* out, hipStream_t st) {
+  const int64_t n = d.tokens * d.top_k;
+  const int blocks = (int)((n + 255) / 256);
+  if (d.act_dtype == KMOE_DTYPE_BF16)
+    hipLaunchKernelGGL((k_cast_from_f32<uint16_t>), dim3(blocks), dim3(256), 0, st, n, topk_w,
+                       reinterpret_cast<uint16_t*>(out));
+  else
+    hipLaunchKernelGGL((k_cast_from_f32<float>), dim3(blocks), dim3(256), 0, st, n, topk_w,
+                       reinterpret_cast<float*>(out));
+  return hipGetLastError();
+}
+
+}  // namespace kmoe_host

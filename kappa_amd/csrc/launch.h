@@ -1,0 +1,41 @@
+// Host-side launch wrappers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "kmoe.h"
+
+namespace kmoe_host {
+
+// route.hip
+hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* logits, int32_t* topk_idx,
+                        float* topk_w, int32_t* hist, hipStream_t st);
+hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const int32_t* hist, int32_t* group_sizes,
+                           int32_t* offsets, int32_t* active, int32_t* sorted_token, int32_t* sorted_expert,
+                           int32_t* inv, hipStream_t st);
+
+// expert.hip
+// Stage selection bits for the expert launchers.
+constexpr int kStageGateUp = 1;  // x -> h_sorted (gate/up products + SwiGLU)
+constexpr int kStageDown = 2;    // h_sorted -> y_sorted (down product)
+// Packed int8 experts on MFMA; decode=true selects the small-T kernels.
+hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, const void* x, const int32_t* offsets,
+                                const int32_t* active, const int32_t* sorted_token, const kmoe_packed_experts& p,
+                                void* h_sorted, void* y_sorted, hipStream_t st);
+// Layout-native experts (any weight kind), one sequential fmaf chain per output.
+hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, const int32_t* sorted_token,
+                                 const int32_t* sorted_expert, const kmoe_weight* gate, const kmoe_weight* up,
+                                 const kmoe_weight* down, void* h_sorted, void* y_sorted, hipStream_t st);
+hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
+                          hipStream_t st);
+hipError_t launch_topk_w_cast(const kmoe_desc& d, const float* topk_w, void* out, hipStream_t st);
+
+// weights.hip
+hipError_t launch_prepack(const kmoe_desc& d, const kmoe_weight& gate, const kmoe_weight& up, const kmoe_weight& down,
+                          const kmoe_packed_experts& p, hipStream_t st);
+hipError_t launch_to_compute_dtype(const kmoe_weight& w, int64_t outer, int64_t channels, int64_t rows_per_block,
+                                   kmoe_dtype out_dtype, void* out, hipStream_t st);
+hipError_t launch_quantize_per_channel(int64_t E, int64_t Kd, int64_t N, const void* w, kmoe_dtype w_dtype, int8_t* q,
+                                       float* s, hipStream_t st);
+
+}  // namespace kmoe_host

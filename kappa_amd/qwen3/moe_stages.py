@@ -1,0 +1,121 @@
+"""The block's stages as separate calls (kmoe_route / kmoe_dispatch /
+kmoe_expert_ffn / kmoe_combine), for per-stage parity checks and profiling.
+
+``moe_swiglu_ffn`` chains exactly these stages inside one C call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _lib
+from .ffn_moe import PACK_CACHE, PackedExperts, _desc, _shape, _stream, packable
+from .quant import Weight, weight_struct
+
+
+def route(x_flat: torch.Tensor, router_w: Weight, *, num_experts: int, k: int) -> dict:
+    """Router logits [T,E] f32, top-k indices [T,K] int32, weights [T,K] f32 (rounded to x.dtype), block histogram."""
+    T, D = x_flat.shape
+    dev = x_flat.device
+    x_flat = x_flat.contiguous()
+    desc = _desc(T, D, num_experts, k, 1, x_flat.dtype, 0)
+    r, keep = weight_struct(router_w, dev, n_out=num_experts, n_groups=None, name="router_w")
+    logits = torch.empty((T, num_experts), dtype=torch.float32, device=dev)
+    idx = torch.empty((T, k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    hist = torch.empty(((T + 63) // 64, num_experts), dtype=torch.int32, device=dev)
+    _lib.check(
+        _lib.lib().kmoe_route(
+            desc, x_flat.data_ptr(), r, logits.data_ptr(), None, idx.data_ptr(), w.data_ptr(), hist.data_ptr(),
+            _stream(dev),
+        )
+    )  # fmt: skip
+    return {"logits": logits, "idx": idx, "w": w, "hist": hist}
+
+
+def dispatch(idx: torch.Tensor, hist: torch.Tensor, *, num_experts: int) -> dict:
+    """Stable sort of the (t, j) assignments by expert."""
+    T, k = idx.shape
+    dev = idx.device
+    M = T * k
+    desc = _desc(T, 1, num_experts, k, 1, torch.float32, 0)
+    out = {
+        "group_sizes": torch.empty(num_experts, dtype=torch.int32, device=dev),
+        "offsets": torch.empty(num_experts + 1, dtype=torch.int32, device=dev),
+        "active": torch.empty(num_experts + 1, dtype=torch.int32, device=dev),
+        "sorted_token": torch.empty(M, dtype=torch.int32, device=dev),
+        "sorted_expert": torch.empty(M, dtype=torch.int32, device=dev),
+        "inv": torch.empty(M, dtype=torch.int32, device=dev),
+    }
+    _lib.check(
+        _lib.lib().kmoe_dispatch(
+            desc, idx.contiguous().data_ptr(), hist.contiguous().data_ptr(),
+            *(out[n].data_ptr() for n in ("group_sizes", "offsets", "active", "sorted_token", "sorted_expert", "inv")),
+            _stream(dev),
+        )
+    )  # fmt: skip
+    return out
+
+
+def expert_ffn(
+    x_flat: torch.Tensor,
+    disp: dict,
+    ffn_gate: Weight,
+    ffn_up: Weight,
+    ffn_down: Weight,
+    *,
+    k: int,
+    decode_threshold: int = 64,
+    packed: PackedExperts | None = None,
+    layout_native: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """SwiGLU experts over the sorted rows: (h_sorted [M, I], y_sorted [M, D]) in x.dtype.
+
+    ``layout_native=True`` runs the kernels that read the reference layout
+    directly (one fmaf chain per output) instead of the packed MFMA kernels."""
+    T, D = x_flat.shape
+    E, _, I = _shape(ffn_gate)
+    dev = x_flat.device
+    M = T * k
+    desc = _desc(T, D, E, k, I, x_flat.dtype, decode_threshold)
+    if not layout_native and packed is None and packable(x_flat.dtype, ffn_gate, ffn_up, ffn_down):
+        packed = PACK_CACHE.get(ffn_gate, ffn_up, ffn_down)
+    if layout_native:
+        packed = None
+    g, kg = weight_struct(ffn_gate, dev, n_out=I, n_groups=E, name="ffn_gate")
+    u, ku = weight_struct(ffn_up, dev, n_out=I, n_groups=E, name="ffn_up")
+    d, kd = weight_struct(ffn_down, dev, n_out=D, n_groups=E, name="ffn_down")
+    h = torch.empty((M, I), dtype=x_flat.dtype, device=dev)
+    y = torch.empty((M, D), dtype=x_flat.dtype, device=dev)
+    _lib.check(
+        _lib.lib().kmoe_expert_ffn(
+            desc, x_flat.contiguous().data_ptr(), disp["offsets"].data_ptr(), disp["active"].data_ptr(),
+            disp["sorted_token"].data_ptr(), disp["sorted_expert"].data_ptr(), g, u, d,
+            packed.struct() if packed is not None else None, h.data_ptr(), y.data_ptr(), _stream(dev),
+        )
+    )  # fmt: skip
+    return h, y
+
+
+def combine(y_sorted: torch.Tensor, inv: torch.Tensor, w: torch.Tensor, *, k: int) -> torch.Tensor:
+    """out[t] = round(sum_j w[t,j] * y_sorted[inv[t*K+j]])."""
+    M, D = y_sorted.shape
+    T = M // k
+    dev = y_sorted.device
+    desc = _desc(T, D, 1 if k == 1 else k, k, 1, y_sorted.dtype, 0)
+    out = torch.empty((T, D), dtype=y_sorted.dtype, device=dev)
+    _lib.check(
+        _lib.lib().kmoe_combine(
+            desc, y_sorted.contiguous().data_ptr(), inv.contiguous().data_ptr(),
+            w.to(torch.float32).contiguous().data_ptr(), out.data_ptr(), _stream(dev),
+        )
+    )  # fmt: skip
+    return out
+
+
+def workspace_bytes(T: int, D: int, E: int, k: int, I: int, act: torch.dtype) -> int:
+    n = ctypes.c_size_t()
+    _lib.check(_lib.lib().kmoe_workspace_bytes(_desc(T, D, E, k, I, act, 64), ctypes.byref(n)))
+    return int(n.value)

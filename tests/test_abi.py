@@ -1,0 +1,160 @@
+"""The C ABI on the host (CPU): exports, argument validation and error statuses.
+
+No compute call runs here: every call either fails validation before touching
+HIP, or reaches the device check and reports that no device is visible (this
+suite also runs where there is no GPU)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT, gpu_available
+from kappa_amd import _lib
+
+HEADER = os.path.join(ROOT, "include", "kmoe.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kmoe_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 15
+    assert sorted(_lib.EXPORTS) == names
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_version_and_status_strings():
+    L = _lib.lib()
+    assert L.kmoe_abi_version() == 1
+    assert b"gfx950" in L.kmoe_version()
+    for s in range(6):
+        assert L.kmoe_status_string(s)
+    assert L.kmoe_status_string(99) == b"unknown status"
+
+
+def desc(T=4, D=128, E=8, K=2, I=64, act=_lib.DTYPE_BF16, thr=64):
+    return _lib.KmoeDesc(T, D, E, K, I, act, thr)
+
+
+def status_and_msg(st):
+    return st, _lib.lib().kmoe_last_error().decode()
+
+
+@pytest.mark.parametrize(
+    "kw,frag",
+    [
+        (dict(T=-1), "tokens"),
+        (dict(D=0), "hidden"),
+        (dict(K=0), "top_k"),
+        (dict(K=9), "top_k"),
+        (dict(act=_lib.DTYPE_I8), "act_dtype"),
+    ],
+)
+def test_workspace_bytes_rejects_bad_desc(kw, frag):
+    n = ctypes.c_size_t()
+    st, msg = status_and_msg(_lib.lib().kmoe_workspace_bytes(desc(**kw), ctypes.byref(n)))
+    assert st == _lib.ERR_INVALID_ARG and frag in msg
+
+
+def test_unsupported_sizes():
+    n = ctypes.c_size_t()
+    L = _lib.lib()
+    assert L.kmoe_workspace_bytes(desc(E=2048, K=2), ctypes.byref(n)) == _lib.ERR_UNSUPPORTED
+    assert L.kmoe_workspace_bytes(desc(D=8192), ctypes.byref(n)) == _lib.ERR_UNSUPPORTED
+    sizes = _lib.KmoePackedSizes()
+    assert L.kmoe_prepack_bytes(desc(D=96), sizes) == _lib.ERR_UNSUPPORTED
+
+
+def test_workspace_and_packed_sizes():
+    L = _lib.lib()
+    n = ctypes.c_size_t()
+    assert L.kmoe_workspace_bytes(desc(T=4096, D=2048, E=128, K=8, I=768), ctypes.byref(n)) == _lib.OK
+    M = 4096 * 8
+    assert n.value >= 2 * M * (768 + 2048) + 4 * 4096 * 128
+    sizes = _lib.KmoePackedSizes()
+    assert L.kmoe_prepack_bytes(desc(D=2048, E=128, I=768), sizes) == _lib.OK
+    assert sizes.w13_bytes == 2 * 128 * 2048 * 768 and sizes.w2_bytes == 128 * 2048 * 768
+    assert sizes.s13_bytes == 4 * 2 * 128 * 768 and sizes.s2_bytes == 4 * 128 * 2048
+
+
+def weight(values=1, dtype=_lib.DTYPE_I8, scale=1, sdtype=_lib.DTYPE_F32, kind=_lib.SCALE_CHANNEL):
+    return _lib.KmoeWeight(values, dtype, scale, sdtype, kind)
+
+
+def test_forward_validation_before_any_hip_call():
+    L = _lib.lib()
+    d = desc()
+    w = weight()
+    f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
+    cases = [
+        (dict(router=weight(values=None)), _lib.ERR_INVALID_ARG, "router values"),
+        (dict(router=weight(kind=_lib.SCALE_NONE)), _lib.ERR_INVALID_ARG, "TENSOR or CHANNEL"),
+        (dict(router=weight(scale=None)), _lib.ERR_INVALID_ARG, "scale pointer"),
+        (dict(router=weight(dtype=_lib.DTYPE_BF16)), _lib.ERR_INVALID_ARG, "takes no scale"),
+        (dict(x=None), _lib.ERR_INVALID_ARG, "x and out"),
+        (dict(ws=None), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
+        (dict(ws_bytes=16), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
+    ]
+    for over, want, frag in cases:
+        a = dict(router=f, x=1, ws=1, ws_bytes=1 << 40)
+        a.update(over)
+        st = L.kmoe_forward(d, a["x"], a["router"], w, w, w, None, 1, None, None, a["ws"], a["ws_bytes"], None)
+        msg = L.kmoe_last_error().decode()
+        assert st == want and frag in msg, (over, st, msg)
+
+
+@pytest.mark.skipif(gpu_available(), reason="checks the no-device status")
+def test_valid_call_without_device_reports_no_device():
+    L = _lib.lib()
+    w = weight()
+    f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
+    st = L.kmoe_forward(desc(), 1, f, w, w, w, None, 1, None, None, 1, 1 << 40, None)
+    assert st == _lib.ERR_NO_DEVICE
+    assert "no HIP device" in L.kmoe_last_error().decode()
+    assert L.kmoe_device_check() == _lib.ERR_NO_DEVICE
+
+
+def test_packed_argument_rules():
+    L = _lib.lib()
+    w = weight()
+    f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
+    p = _lib.KmoePacked(1, 1, 1, None)
+    st = L.kmoe_forward(desc(), 1, f, w, w, w, p, 1, None, None, 1, 1 << 40, None)
+    assert st == _lib.ERR_INVALID_ARG
+    p = _lib.KmoePacked(1, 1, 1, 1)
+    st = L.kmoe_forward(desc(act=_lib.DTYPE_F32), 1, f, w, w, w, p, 1, None, None, 1, 1 << 40, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    st = L.kmoe_forward(desc(D=96), 1, f, w, w, w, p, 1, None, None, 1, 1 << 40, None)
+    assert st == _lib.ERR_UNSUPPORTED
+
+
+def test_stage_entry_points_validate():
+    L = _lib.lib()
+    f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
+    assert L.kmoe_route(desc(), 1, f, None, None, 1, 1, 1, None) == _lib.ERR_INVALID_ARG
+    assert L.kmoe_dispatch(desc(), 1, 1, 1, 1, 1, 1, 1, None, None) == _lib.ERR_INVALID_ARG
+    assert L.kmoe_combine(desc(), 1, None, 1, 1, None) == _lib.ERR_INVALID_ARG
+    assert L.kmoe_expert_ffn(desc(), 1, 1, 1, 1, 1, None, None, None, None, 1, 1, None) == _lib.ERR_INVALID_ARG
+    i8 = weight()
+    assert L.kmoe_prepack(desc(), f, i8, i8, _lib.KmoePacked(1, 1, 1, 1), None) == _lib.ERR_UNSUPPORTED
+    assert L.kmoe_to_compute_dtype(i8, 4, 0, 1, _lib.DTYPE_BF16, 1, None) == _lib.ERR_INVALID_ARG
+    assert L.kmoe_quantize_per_channel(1, 4, 4, 1, _lib.DTYPE_I8, 1, 1, None) == _lib.ERR_INVALID_ARG
+
+
+def test_zero_tokens_is_a_no_op_after_validation():
+    if gpu_available():
+        pytest.skip("the device check passes on a GPU host")
+    L = _lib.lib()
+    w = weight()
+    f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
+    # T = 0 still validates, then reports the missing device (no launch is attempted)
+    st = L.kmoe_forward(desc(T=0), 1, f, w, w, w, None, 1, None, None, None, 0, None)
+    assert st == _lib.ERR_NO_DEVICE

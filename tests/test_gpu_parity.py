@@ -1,0 +1,310 @@
+"""HIP kernels against the oracle (GPU).
+
+Bar: top-k indices and the dispatch arrays bit-exact; router logits bit-exact
+(the kernels and the oracle share the canonical summation order); layer
+outputs within max-abs 2e-2 and mean-rel 1e-3 in bf16, 1e-5 (relative to the
+output scale) in f32. mean-rel = mean|a - b| / mean|b|.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from inputs import GOLDEN_SPECS, Spec, make_inputs
+from moe_cases import bf16_np, make_layer, make_x, mean_rel, oracle_rows, skew_router
+
+pytestmark = pytest.mark.gpu
+
+BF16_MAX_ABS = 2e-2
+BF16_MEAN_REL = 1e-3
+F32_REL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    return torch.device("cuda:0")
+
+
+def to_dev_weight(w, dev, act_bf16):
+    from kappa_amd.qwen3 import Q8Weight
+
+    if isinstance(w, tuple):
+        q, s = w
+        return Q8Weight(torch.from_numpy(np.ascontiguousarray(q)).to(dev), torch.as_tensor(np.asarray(s, np.float32)).to(dev))
+    t = torch.from_numpy(np.ascontiguousarray(w, np.float32)).to(dev)
+    return t.to(torch.bfloat16) if act_bf16 else t
+
+
+def spec_to_dev(spec: Spec, inp: dict, dev):
+    bf16 = spec.act == "bf16"
+    x = torch.from_numpy(inp["x"]).to(dev)
+    x = x.to(torch.bfloat16) if bf16 else x
+    r = inp["router"]
+    if isinstance(r, tuple):
+        rd = to_dev_weight(r, dev, bf16)
+    else:
+        rd = torch.from_numpy(r).to(dev)
+        rd = rd.to(torch.bfloat16) if spec.router == "bf16" else rd
+    ws = [to_dev_weight(inp[n], dev, spec.weights == "bf16") for n in ("gate", "up", "down")]
+    if spec.weights == "f32":
+        ws = [torch.from_numpy(inp[n]).to(dev) for n in ("gate", "up", "down")]
+    return x, rd, ws
+
+
+def check_out(out: np.ndarray, ref: np.ndarray, bf16: bool, what: str = "out"):
+    if bf16:
+        d = np.abs(out - ref)
+        assert d.max() <= BF16_MAX_ABS, f"{what}: max-abs {d.max():.3e}"
+        assert mean_rel(out, ref) <= BF16_MEAN_REL, f"{what}: mean-rel {mean_rel(out, ref):.3e}"
+    else:
+        scale = max(float(np.abs(ref).max()), 1e-30)
+        assert np.abs(out - ref).max() <= F32_REL * scale, f"{what}: {np.abs(out - ref).max() / scale:.3e}"
+
+
+# --- golden cases: the whole block through moe_swiglu_ffn ----------------------
+
+
+@pytest.mark.parametrize("spec", GOLDEN_SPECS, ids=[s.name for s in GOLDEN_SPECS])
+def test_golden_block(dev, spec):
+    from kappa_amd.qwen3 import moe_layer_config
+    from kappa_amd.qwen3.ffn_moe import _moe_forward
+
+    inp = make_inputs(spec)
+    bf16 = spec.act == "bf16"
+    x, r, (g, u, d) = spec_to_dev(spec, inp, dev)
+    out, idx, w = _moe_forward(
+        x.reshape(1, spec.T, spec.D), r, g, u, d, num_experts=spec.E, num_experts_per_tok=spec.K,
+        decode_threshold=64, packed=None, return_routing=True,
+    )  # fmt: skip
+    ref = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=bf16)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref["idx"])
+    wg = w.float().cpu().numpy()
+    assert np.all(np.abs(wg - ref["w"]) <= (2.0**-8 if bf16 else 2.0**-22) * np.abs(ref["w"]))
+    check_out(out.reshape(spec.T, spec.D).float().cpu().numpy(), ref["out"], bf16)
+    # and against the golden vectors written from the reference restatement
+    gold = np.load(f"tests/golden/{spec.name}.npz")
+    np.testing.assert_array_equal(idx.cpu().numpy(), gold["idx"])
+    check_out(out.reshape(spec.T, spec.D).float().cpu().numpy(), gold["out"], bf16, "vs golden")
+
+
+# --- the 30B-A3B and 235B-A22B layers ----------------------------------------
+
+
+@pytest.fixture(scope="module")
+def l30(dev):
+    return make_layer("30b", seed=0)
+
+
+def _route_and_dispatch(x, layer_router, E, K):
+    from kappa_amd.qwen3 import moe_stages
+
+    r = moe_stages.route(x, layer_router, num_experts=E, k=K)
+    d = moe_stages.dispatch(r["idx"], r["hist"], num_experts=E)
+    return r, d
+
+
+def _check_routing(x, router, E, K, r, d):
+    xn = bf16_np(x)
+    rn = router.float().cpu().numpy()
+    lg = oracle.router_logits(xn, rn)
+    np.testing.assert_array_equal(r["logits"].cpu().numpy(), lg)  # canonical order: bit-exact
+    idx, w = oracle.topk_softmax(lg, K, act_bf16=True)
+    np.testing.assert_array_equal(r["idx"].cpu().numpy(), idx)
+    wd = r["w"].cpu().numpy()
+    assert np.mean(wd != w) < 1e-3 and np.all(np.abs(wd - w) <= 2.0**-8 * w)
+    od = oracle.dispatch(idx, E)
+    for n in ("group_sizes", "offsets", "sorted_token", "inv"):
+        np.testing.assert_array_equal(d[n].cpu().numpy(), od[n], err_msg=n)
+    np.testing.assert_array_equal(d["sorted_expert"].cpu().numpy(), idx.reshape(-1)[od["order"]])
+    act = np.nonzero(od["group_sizes"])[0]
+    a = d["active"].cpu().numpy()
+    assert a[E] == len(act)
+    np.testing.assert_array_equal(a[: len(act)], act)
+    return xn, idx, w, od
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 64])
+def test_30b_decode_full(dev, l30, T):
+    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+
+    x = make_x(T, l30.D, seed=T)
+    r, d = _route_and_dispatch(x, l30.router, l30.E, l30.K)
+    xn, idx, w, od = _check_routing(x, l30.router, l30.E, l30.K, r, d)
+    host = l30.host()
+    h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K)
+    ho, yo = oracle.expert_ffn(xn, od["offsets"], od["sorted_token"], host["gate"], host["up"], host["down"], True)
+    check_out(bf16_np(h), ho, True, "h")
+    check_out(bf16_np(y), yo, True, "y")
+    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
+    out = moe_swiglu_ffn(x.reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
+    ref = oracle.combine(yo, od["inv"], w, True)
+    check_out(bf16_np(out.reshape(T, l30.D)), ref, True)
+
+
+@pytest.mark.parametrize("T", [512, 2048, 4096])
+def test_30b_prefill_sampled(dev, l30, T):
+    _prefill_sampled(l30, T, seed=100 + T)
+
+
+def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48):
+    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+
+    router = layer.router if router is None else router
+    x = make_x(T, layer.D, seed=seed) if x is None else x
+    r, d = _route_and_dispatch(x, router, layer.E, layer.K)
+    xn, idx, w, od = _check_routing(x, router, layer.E, layer.K, r, d)
+    h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K)
+    cfg = moe_layer_config(hidden=layer.D, experts=layer.E, top_k=layer.K, intermediate=layer.I)
+    out = moe_swiglu_ffn(x.reshape(1, T, layer.D), router, layer.gate, layer.up, layer.down, cfg=cfg)
+    rng = np.random.default_rng(seed)
+    toks = np.sort(rng.choice(T, size=min(n_tok, T), replace=False))
+    toks = np.unique(np.concatenate([toks, [0, T - 1]]))
+    rows_t = np.repeat(toks, layer.K)
+    rows_e = idx[toks].reshape(-1)
+    ho, yo = oracle_rows(oracle, xn, rows_t, rows_e, layer.host())
+    pos = od["inv"].reshape(T, layer.K)[toks].reshape(-1)
+    check_out(bf16_np(h)[pos], ho, True, "h rows")
+    check_out(bf16_np(y)[pos], yo, True, "y rows")
+    ref = oracle.combine(yo, np.arange(len(rows_t), dtype=np.int32), w[toks], True)
+    check_out(bf16_np(out.reshape(T, layer.D))[toks], ref, True, "out rows")
+    return od
+
+
+def test_30b_skewed_routing(dev, l30):
+    for T, seed in ((4096, 7), (64, 8)):
+        x = make_x(T, l30.D, seed=seed)
+        x[:, 0] = 1.0
+        router = skew_router(l30.router, lam=1.5)
+        od = _prefill_sampled(l30, T, seed, router=router, x=x)
+        share = np.sort(od["group_sizes"])[::-1][:8].sum() / (T * l30.K)
+        assert share > 0.5, f"hot-expert share {share:.2f}"
+
+
+def test_235b_layer(dev):
+    layer = make_layer("235b", seed=1)
+    _prefill_sampled(layer, 16, seed=16, n_tok=16)
+    _prefill_sampled(layer, 2048, seed=2048, n_tok=24)
+    del layer
+    torch.cuda.empty_cache()
+
+
+# --- cross-checks between kernel families, determinism, edge cases -----------
+
+
+def test_decode_and_prefill_kernels_agree_at_threshold(dev, l30):
+    from kappa_amd.qwen3 import moe_layer_config, moe_swiglu_ffn
+
+    for T in (64, 65):
+        x = make_x(T, l30.D, seed=300 + T).reshape(1, T, l30.D)
+        outs = []
+        for thr in (64, 0):
+            cfg = moe_layer_config(
+                hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_ragged_decode_token_threshold=thr
+            )
+            outs.append(bf16_np(moe_swiglu_ffn(x, l30.router, l30.gate, l30.up, l30.down, cfg=cfg)))
+        check_out(outs[0], outs[1], True, f"T={T}")
+
+
+def test_layout_native_experts_match_packed(dev, l30):
+    from kappa_amd.qwen3 import moe_stages
+
+    for T in (8, 200):
+        x = make_x(T, l30.D, seed=400 + T)
+        r, d = _route_and_dispatch(x, l30.router, l30.E, l30.K)
+        h1, y1 = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K)
+        h2, y2 = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K, layout_native=True)
+        check_out(bf16_np(h1), bf16_np(h2), True, "h")
+        check_out(bf16_np(y1), bf16_np(y2), True, "y")
+
+
+def test_repeat_runs_are_bitwise_identical(dev, l30):
+    from kappa_amd.qwen3 import moe_layer_config, moe_swiglu_ffn
+
+    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
+    for T in (7, 333):
+        x = make_x(T, l30.D, seed=500 + T).reshape(1, T, l30.D)
+        a = moe_swiglu_ffn(x, l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
+        b = moe_swiglu_ffn(x, l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T", [0, 3, 65, 1000])
+def test_ragged_token_counts(dev, T):
+    from kappa_amd.qwen3 import moe_layer_config, moe_swiglu_ffn
+
+    spec = Spec("ragged", T=max(T, 1), D=128, E=16, K=4, I=64, base_seed=80 + T)
+    inp = make_inputs(spec)
+    x, r, (g, u, d) = spec_to_dev(spec, inp, dev)
+    x = x[:T].reshape(1, T, spec.D)
+    cfg = moe_layer_config(hidden=128, experts=16, top_k=4, intermediate=64)
+    out = moe_swiglu_ffn(x, r, g, u, d, cfg=cfg)
+    assert out.shape == (1, T, 128) and out.dtype == torch.bfloat16
+    if T:
+        ref = oracle.forward(inp["x"][:T], inp["router"], inp["gate"], inp["up"], inp["down"], k=4, act_bf16=True)
+        check_out(bf16_np(out.reshape(T, 128)), ref["out"], True)
+
+
+# --- weights ------------------------------------------------------------------
+
+
+def test_quantiser_matches_oracle(dev):
+    from kappa_amd.qwen3 import quantize_weight_per_channel
+
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((3, 512, 96)) * 0.02).astype(np.float32)
+    q, s = quantize_weight_per_channel(torch.from_numpy(w).to(dev))
+    qo, so = oracle.quantize_per_channel(w)
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy(), so)
+    wb = torch.from_numpy(w).to(dev).to(torch.bfloat16)
+    q2, s2 = quantize_weight_per_channel(wb)
+    qo2, so2 = oracle.quantize_per_channel(wb.float().cpu().numpy())
+    np.testing.assert_array_equal(q2.cpu().numpy(), qo2)
+    np.testing.assert_array_equal(s2.cpu().numpy(), so2)
+
+
+def test_to_compute_dtype_matches_reference_rule(dev):
+    from kappa_amd.qwen3 import Q8Weight, to_compute_dtype
+
+    rng = np.random.default_rng(13)
+    q = rng.integers(-128, 128, (4, 64, 48)).astype(np.int8)
+    s = (rng.random((4, 1, 48)) * 0.01).astype(np.float32)
+    w = Q8Weight(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev))
+    bf = to_compute_dtype(w, torch.bfloat16).float().cpu().numpy()
+    ref = oracle.bf16_round(q.astype(np.float32) * oracle.bf16_round(s))
+    np.testing.assert_array_equal(bf, ref)
+    f32 = to_compute_dtype(w, torch.float32).cpu().numpy()
+    np.testing.assert_array_equal(f32, q.astype(np.float32) * s)
+    wt = Q8Weight(torch.from_numpy(q).to(dev), torch.tensor(0.0123, dtype=torch.bfloat16, device=dev))
+    st = np.float32(torch.tensor(0.0123, dtype=torch.bfloat16).float().item())
+    np.testing.assert_array_equal(
+        to_compute_dtype(wt, torch.bfloat16).float().cpu().numpy(), oracle.bf16_round(q.astype(np.float32) * st)
+    )
+
+
+def test_prepack_layout(dev):
+    from kappa_amd.qwen3 import Q8Weight, prepack_moe_experts
+
+    rng = np.random.default_rng(14)
+    E, D, I = 3, 128, 64
+    qs = [rng.integers(-128, 128, shp).astype(np.int8) for shp in ((E, D, I), (E, D, I), (E, I, D))]
+    ss = [(rng.random((E, 1, n)) * 0.01).astype(np.float32) for n in (I, I, D)]
+    ws = [Q8Weight(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)) for q, s in zip(qs, ss)]
+    p = prepack_moe_experts(*ws)
+    w13 = p.w13.cpu().numpy().reshape(E, I // 16, 2, D // 16, 16, 16)
+    # cell [e, ig, which, kg, col, kk] = src[e, kg*16+kk, ig*16+col]
+    for which in (0, 1):
+        src = qs[which].reshape(E, D // 16, 16, I // 16, 16)  # e, kg, kk, ig, col
+        np.testing.assert_array_equal(w13[:, :, which], src.transpose(0, 3, 1, 4, 2))
+    w2 = p.w2.cpu().numpy().reshape(E, D // 16, I // 16, 16, 16)
+    src = qs[2].reshape(E, I // 16, 16, D // 16, 16)  # e, kg, kk, dg, col
+    np.testing.assert_array_equal(w2, src.transpose(0, 3, 1, 4, 2))
+    s13 = p.s13.cpu().numpy().reshape(E, I // 16, 2, 16)
+    for which in (0, 1):
+        np.testing.assert_array_equal(s13[:, :, which], oracle.bf16_round(ss[which]).reshape(E, I // 16, 16))
+    np.testing.assert_array_equal(p.s2.cpu().numpy().reshape(E, D), oracle.bf16_round(ss[2]).reshape(E, D))

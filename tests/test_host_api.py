@@ -1,0 +1,61 @@
+"""The Python boundary mirrors the reference's errors (CPU; no compute)."""
+
+import dataclasses
+
+import pytest
+import torch
+
+from kappa_amd.qwen3 import Q8Weight, moe_layer_config, moe_swiglu_ffn, qwen3_config_for_preset
+from kappa_amd.qwen3.ffn_moe import _effective_moe_impl
+
+
+def cfg(**kw):
+    return moe_layer_config(hidden=16, experts=8, top_k=2, intermediate=32, **kw)
+
+
+def args(d=16, e=8, i=32):
+    x = torch.zeros(2, 3, d)
+    return x, torch.zeros(d, e), torch.zeros(e, d, i), torch.zeros(e, d, i), torch.zeros(e, i, d)
+
+
+def test_requires_use_moe():
+    with pytest.raises(ValueError, match="moe_swiglu_ffn requires cfg.use_moe"):
+        moe_swiglu_ffn(*args(), cfg=cfg(use_moe=False))
+
+
+def test_router_shape_message_matches_reference():
+    x, r, g, u, d = args()
+    with pytest.raises(ValueError, match=r"router_w shape \(16, 4\) != \(16, 8\)"):
+        moe_swiglu_ffn(x, torch.zeros(16, 4), g, u, d, cfg=cfg())
+    q = Q8Weight(torch.zeros(8, 16, dtype=torch.int8), torch.tensor(1.0))
+    with pytest.raises(ValueError, match=r"router_w shape \(8, 16\) != \(16, 8\)"):
+        moe_swiglu_ffn(x, q, g, u, d, cfg=cfg())
+
+
+def test_unknown_impl_and_capacity_errors():
+    with pytest.raises(ValueError, match="unknown moe_impl: 'bogus'"):
+        moe_swiglu_ffn(*args(), cfg=cfg(moe_impl="bogus"))
+    with pytest.raises(ValueError, match="fixed_capacity requires cfg.moe_capacity_factor > 0"):
+        moe_swiglu_ffn(*args(), cfg=cfg(moe_impl="fixed_capacity", moe_capacity_factor=0.0))
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    with pytest.raises(ValueError, match="HIP device"):
+        moe_swiglu_ffn(*args(), cfg=cfg())
+
+
+def test_effective_impl_mirrors_reference_threshold():
+    c = cfg(moe_impl="ragged_jax")
+    assert _effective_moe_impl(c, total_tokens=64) == "gather_einsum"
+    assert _effective_moe_impl(c, total_tokens=65) == "ragged_jax"
+    assert _effective_moe_impl(cfg(), total_tokens=4096) == "gather_einsum"
+    c0 = dataclasses.replace(c, moe_ragged_decode_token_threshold=0)
+    assert _effective_moe_impl(c0, total_tokens=1) == "ragged_jax"
+
+
+def test_presets_match_reference_values():
+    c = qwen3_config_for_preset("qwen3-30b-a3b")
+    assert (c.model_dim, c.num_experts, c.num_experts_per_tok, c.intermediate_size) == (2048, 128, 8, 768)
+    assert c.moe_impl == "gather_einsum" and c.moe_ragged_decode_token_threshold == 64
+    with pytest.raises(ValueError, match="unknown preset"):
+        qwen3_config_for_preset("nope")

@@ -1,0 +1,86 @@
+"""The oracle against the golden vectors (CPU).
+
+The golden vectors in tests/golden/ were written by make_golden.py, a numpy /
+torch-CPU transliteration of the reference's array program
+(kappa/qwen3/ffn_moe.py:38-104, 189-215; kappa/qwen3/quant.py:34-38, 60-76)
+with float64 accumulation. The C oracle accumulates in float32 in its own
+order, so floating results agree to rounding, and integer results exactly.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from inputs import GOLDEN_SPECS, digest, make_inputs
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+META = json.load(open(os.path.join(HERE, "golden.json")))
+
+
+@pytest.mark.parametrize("spec", GOLDEN_SPECS, ids=[s.name for s in GOLDEN_SPECS])
+def test_oracle_matches_golden(spec):
+    inp = make_inputs(spec)
+    assert digest(inp) == META[spec.name]["input_sha256"], "input generator drifted from the golden vectors"
+    g = np.load(os.path.join(HERE, f"{spec.name}.npz"))
+    bf16 = spec.act == "bf16"
+    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=bf16)
+    # logits: fp32 canonical order vs fp64 within the fp32 summation error bound
+    rw = inp["router"]
+    rf = (rw[0].astype(np.float64) * np.float64(rw[1])) if isinstance(rw, tuple) else rw.astype(np.float64)
+    bound = 2.0 * spec.D * np.finfo(np.float32).eps * (np.abs(inp["x"]).astype(np.float64) @ np.abs(rf)) + 1e-30
+    assert np.all(np.abs(r["logits"] - g["logits64"]) <= bound)
+    # top-k indices and dispatch are integer results: exact
+    np.testing.assert_array_equal(r["idx"], g["idx"])
+    np.testing.assert_array_equal(r["order"], g["order"])
+    np.testing.assert_array_equal(r["group_sizes"], g["group_sizes"])
+    np.testing.assert_array_equal(r["inv"], g["inv"])
+    np.testing.assert_array_equal(r["sorted_token"], g["order"] // spec.K)
+    # routing weights: within one ulp of the activation dtype
+    ulp = 2.0**-8 if bf16 else 2.0**-23
+    assert np.all(np.abs(r["w"] - g["w"]) <= ulp * np.abs(g["w"]) + 1e-30)
+    # expert outputs in gather order [T, K, D]
+    y_g = r["y_sorted"][r["inv"]].reshape(spec.T, spec.K, -1)
+    h_g = r["h_sorted"][r["inv"]].reshape(spec.T, spec.K, -1)
+    out = r["out"]
+    if bf16:
+        # identical except rare one-ulp flips from fp32 vs fp64 accumulation
+        for a, b in ((h_g, g["h"]), (y_g, g["y_k"]), (out, g["out"])):
+            diff = np.abs(a - b)
+            assert np.mean(diff > 0) < 2e-3
+            assert np.all(diff <= 2.0**-7 * np.abs(b) + 1e-6)
+    else:
+        scale = max(float(np.abs(g["out"]).max()), 1e-30)
+        assert np.max(np.abs(out - g["out"])) <= 1e-5 * scale
+        assert np.max(np.abs(y_g - g["y_k"])) <= 1e-5 * max(float(np.abs(g["y_k"]).max()), 1e-30)
+
+
+def test_golden_cases_have_no_near_ties_except_the_tie_kats():
+    for spec in GOLDEN_SPECS:
+        gap = META[spec.name]["min_gap"]
+        if spec.name.startswith("tie_"):
+            assert gap == 0.0
+        else:
+            assert gap > 1e-4, spec.name
+
+
+def test_tie_kats():
+    # x = 0: every logit is +0.0, so top-k is [0..K-1] and each weight is round(1/K)
+    spec = next(s for s in GOLDEN_SPECS if s.name == "tie_zero_x")
+    inp = make_inputs(spec)
+    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=True)
+    np.testing.assert_array_equal(r["idx"], np.tile(np.arange(spec.K, dtype=np.int32), (spec.T, 1)))
+    np.testing.assert_array_equal(r["w"], oracle.bf16_round(np.full((spec.T, spec.K), 1.0 / spec.K, np.float32)))
+    assert np.all(r["out"] == 0.0)
+    # duplicated router columns: experts e and e+4 tie exactly; the lower index comes first
+    spec = next(s for s in GOLDEN_SPECS if s.name == "tie_router")
+    inp = make_inputs(spec)
+    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=True)
+    lg = r["logits"]
+    np.testing.assert_array_equal(lg[:, :4], lg[:, 4:])
+    for t in range(spec.T):
+        best = int(np.argmax(lg[t, :4]))
+        assert r["idx"][t, 0] == best and r["idx"][t, 1] == best + 4
+        assert r["w"][t, 0] == r["w"][t, 1]
