@@ -318,7 +318,7 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
     KMOE_TRY(check_weight(up, "up"));
     KMOE_TRY(check_weight(down, "down"));
   }
-  if (!x || !out) return fail(KMOE_ERR_INVALID_ARG, "kmoe_forward: x and out must be non-NULL");
+  if (desc->tokens > 0 && (!x || !out)) return fail(KMOE_ERR_INVALID_ARG, "kmoe_forward: x and out must be non-NULL");
   const Workspace w = layout(*desc);
   if (desc->tokens > 0 && (!workspace || workspace_bytes < w.total))
     return fail(KMOE_ERR_WORKSPACE_TOO_SMALL, "workspace of %zu bytes is smaller than the %zu required",

@@ -66,6 +66,26 @@ def check_out(out: np.ndarray, ref: np.ndarray, bf16: bool, what: str = "out"):
         assert np.abs(out - ref).max() <= F32_REL * scale, f"{what}: {np.abs(out - ref).max() / scale:.3e}"
 
 
+def check_inter(out: np.ndarray, ref: np.ndarray, what: str):
+    """bf16 intermediates (h, y).
+
+    The MFMA kernels and the oracle add the same products in different fp32 orders, so
+    g, u and y may round to a neighbouring bf16 number; silu amplifies a flip in g (up to
+    ~4x near g = -5) and y has cancellation near zero, so an elementwise ulp bound does not
+    apply. The bar: mean-rel <= 1e-3, every difference within 4 bf16 ulps of the tensor's
+    largest magnitude, and at most 10% of elements not bit-identical (a wrong rounding
+    point or scale changes most elements)."""
+    d = np.abs(out - ref)
+    top = float(np.abs(ref).max())
+    diff_frac = float(np.mean(d > 0))
+    print(f"{what}: mean-rel {mean_rel(out, ref):.2e} max-abs {d.max():.2e} (max|ref| {top:.2e}) "
+          f"not-identical {diff_frac:.4f}")
+    assert mean_rel(out, ref) <= BF16_MEAN_REL, f"{what}: mean-rel {mean_rel(out, ref):.3e}"
+    assert d.max() <= 2.0**-6 * top, f"{what}: max-abs {d.max():.3e} vs max|ref| {top:.3e}"
+    assert diff_frac <= 0.10, f"{what}: {diff_frac:.3f} of elements differ"
+
+
+
 # --- golden cases: the whole block through moe_swiglu_ffn ----------------------
 
 
@@ -138,8 +158,8 @@ def test_30b_decode_full(dev, l30, T):
     host = l30.host()
     h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K)
     ho, yo = oracle.expert_ffn(xn, od["offsets"], od["sorted_token"], host["gate"], host["up"], host["down"], True)
-    check_out(bf16_np(h), ho, True, "h")
-    check_out(bf16_np(y), yo, True, "y")
+    check_inter(bf16_np(h), ho, "h")
+    check_inter(bf16_np(y), yo, "y")
     cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
     out = moe_swiglu_ffn(x.reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
     ref = oracle.combine(yo, od["inv"], w, True)
@@ -168,8 +188,8 @@ def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48):
     rows_e = idx[toks].reshape(-1)
     ho, yo = oracle_rows(oracle, xn, rows_t, rows_e, layer.host())
     pos = od["inv"].reshape(T, layer.K)[toks].reshape(-1)
-    check_out(bf16_np(h)[pos], ho, True, "h rows")
-    check_out(bf16_np(y)[pos], yo, True, "y rows")
+    check_inter(bf16_np(h)[pos], ho, "h rows")
+    check_inter(bf16_np(y)[pos], yo, "y rows")
     ref = oracle.combine(yo, np.arange(len(rows_t), dtype=np.int32), w[toks], True)
     check_out(bf16_np(out.reshape(T, layer.D))[toks], ref, True, "out rows")
     return od
@@ -218,8 +238,8 @@ def test_layout_native_experts_match_packed(dev, l30):
         r, d = _route_and_dispatch(x, l30.router, l30.E, l30.K)
         h1, y1 = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K)
         h2, y2 = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K, layout_native=True)
-        check_out(bf16_np(h1), bf16_np(h2), True, "h")
-        check_out(bf16_np(y1), bf16_np(y2), True, "y")
+        check_inter(bf16_np(h1), bf16_np(h2), "h")
+        check_inter(bf16_np(y1), bf16_np(y2), "y")
 
 
 def test_repeat_runs_are_bitwise_identical(dev, l30):
