@@ -131,9 +131,9 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
 /* --- stages (per-stage parity; kmoe_forward chains exactly these) ------- */
 /* _route (kappa/qwen3/ffn_moe.py:38-56): logits [T,E] f32 (optional, may be
  * NULL), topk_idx [T,K] int32, topk_w [T,K] f32 holding values already
- * rounded to x.dtype, block_hist [ceil(T/64), E] int32 (per 64-token block
- * expert counts consumed by kmoe_dispatch). `logits_scratch` [T,E] f32 is
- * required when `logits` is NULL. */
+ * rounded to x.dtype, block_hist [ceil(T/64), E] int32 (per 64-token chunk
+ * expert counts consumed by kmoe_dispatch). `logits_scratch` is unused (the
+ * logits never leave the kernel unless `logits` is given) and may be NULL. */
 kmoe_status kmoe_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, float* logits,
                        float* logits_scratch, int32_t* topk_idx, float* topk_w, int32_t* block_hist, void* stream);
 

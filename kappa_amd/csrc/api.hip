@@ -91,7 +91,7 @@ kmoe_status check_weight(const kmoe_weight* w, const char* name, bool allow_int8
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Workspace {
-  size_t logits, topk_idx, topk_w, hist, group_sizes, offsets, active, sorted_token, sorted_expert, inv, h_sorted,
+  size_t topk_idx, topk_w, hist, group_sizes, offsets, active, sorted_token, sorted_expert, inv, h_sorted,
       y_sorted, total;
 };
 
@@ -108,7 +108,6 @@ Workspace layout(const kmoe_desc& d) {
     o = align_up(o + bytes);
     return at;
   };
-  w.logits = take(4 * T * E);
   w.topk_idx = take(4 * M);
   w.topk_w = take(4 * M);
   w.hist = take(4 * nblk * E);
@@ -224,14 +223,14 @@ kmoe_status kmoe_prepack_bytes(const kmoe_desc* desc, kmoe_packed_sizes* sizes) 
 
 kmoe_status kmoe_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, float* logits,
                        float* logits_scratch, int32_t* topk_idx, float* topk_w, int32_t* block_hist, void* stream) {
+  (void)logits_scratch;
   KMOE_TRY(check_desc(desc));
   KMOE_TRY(check_weight(router, "router"));
-  if (!x || !topk_idx || !topk_w || !block_hist || (!logits && !logits_scratch))
-    return fail(KMOE_ERR_INVALID_ARG, "kmoe_route: NULL buffer");
+  if (!x || !topk_idx || !topk_w || !block_hist) return fail(KMOE_ERR_INVALID_ARG, "kmoe_route: NULL buffer");
   KMOE_TRY(device_status());
   if (desc->tokens == 0) return KMOE_OK;
-  hipError_t e = kmoe_host::launch_route(*desc, x, *router, logits ? logits : logits_scratch, topk_idx, topk_w,
-                                         block_hist, (hipStream_t)stream);
+  hipError_t e = kmoe_host::launch_route(*desc, x, *router, logits, topk_idx, topk_w, block_hist,
+                                         (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "route kernels");
   return KMOE_OK;
 }
@@ -327,7 +326,6 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
   if (desc->tokens == 0) return KMOE_OK;
   hipStream_t st = (hipStream_t)stream;
   char* base = reinterpret_cast<char*>(workspace);
-  float* logits = reinterpret_cast<float*>(base + w.logits);
   int32_t* tidx = reinterpret_cast<int32_t*>(base + w.topk_idx);
   float* tw = reinterpret_cast<float*>(base + w.topk_w);
   int32_t* hist = reinterpret_cast<int32_t*>(base + w.hist);
@@ -339,8 +337,10 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
   int32_t* inv = reinterpret_cast<int32_t*>(base + w.inv);
   void* hs = base + w.h_sorted;
   void* ys = base + w.y_sorted;
-  KMOE_HIP(kmoe_host::launch_route(*desc, x, *router, logits, tidx, tw, hist, st), "route kernels");
-  KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, hist, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
+  // one 64-token chunk: the dispatch counts the chunk itself, no histogram pass
+  int32_t* h = desc->tokens > kmoe::kDispatchBlock ? hist : nullptr;
+  KMOE_HIP(kmoe_host::launch_route(*desc, x, *router, nullptr, tidx, tw, h, st), "route kernels");
+  KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, h, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
   KMOE_TRY(expert_stage(*desc, kmoe_host::kStageGateUp | kmoe_host::kStageDown, x, off, act, stok, sexp, gate, up,
                         down, packed, hs, ys, st));
   KMOE_HIP(kmoe_host::launch_combine(*desc, ys, inv, tw, out, st), "combine kernel");

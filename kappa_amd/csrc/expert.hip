@@ -91,34 +91,55 @@ __device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
 // ---------------------------------------------------------------------------
 // Decode (T <= 64): one block per (active expert, 16-column group); the four
 // waves split the reduction axis and are summed in wave order through LDS.
-// Each weight byte is read exactly once per call.
+// Each weight byte is read exactly once per call. A wave issues the weight
+// loads of a batch of NB 64-deep chunks (NB x 1 KB per operand in flight)
+// before anything else - they depend only on the expert - then finds its rows
+// and loads the activation fragments, dequantises and runs the MFMAs; the raw
+// int8 stays in registers across 16-row blocks. GUARD handles a chunk count
+// per wave that NB does not divide.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_gateup_decode(int D, int I, int E, const uint16_t* __restrict__ x,
+template <int WPB, int NB, bool GUARD>
+__global__ __launch_bounds__(512) void k_gateup_decode(int D, int I, int E, const uint16_t* __restrict__ x,
                                                         const int32_t* __restrict__ offsets,
                                                         const int32_t* __restrict__ active,
                                                         const int32_t* __restrict__ sorted_token,
                                                         const int8_t* __restrict__ w13, const float* __restrict__ s13,
                                                         uint16_t* __restrict__ h_sorted) {
-  __shared__ floatx4 red[3][kDecodeMaxRowBlocks][2][64];
+  __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][kDecodeMaxRowBlocks][2][64];
   const int ig = blockIdx.x;
   const int slot = blockIdx.y;
-  if (slot >= active[E]) return;
-  const int e = active[slot];
-  const int r0 = offsets[e];
-  const int nrows = offsets[e + 1] - r0;
-  const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
+  const int n_active = active[E];
+  const int e = active[slot < E ? slot : 0];
+  if (slot >= n_active) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int IG = I >> 4, KC = D >> 6;
   const size_t cell = (size_t)(D >> 4) * 256;
-  const int8_t* bg = w13 + (((size_t)e * IG + ig) * 2 + 0) * cell;
+  const int8_t* bg = w13 + (((size_t)e * IG + ig) * 2 + 0) * cell + lane * 16;
   const int8_t* bu = bg + cell;
+  const int c0 = (KC * wv) / WPB, c1 = (KC * (wv + 1)) / WPB;
+  uint4 qg[NB], qu[NB];
+  auto load_w = [&](int cb) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if (!GUARD || cb + i < c1) {
+        qg[i] = *reinterpret_cast<const uint4*>(bg + (size_t)(cb + i) * 1024);
+        qu[i] = *reinterpret_cast<const uint4*>(bu + (size_t)(cb + i) * 1024);
+      }
+    }
+  };
+  load_w(c0);
   const float sg = s13[(((size_t)e * IG + ig) * 2 + 0) * 16 + (lane & 15)];
   const float su = s13[(((size_t)e * IG + ig) * 2 + 1) * 16 + (lane & 15)];
-  int tok[kDecodeMaxRowBlocks];
+  const int r0 = offsets[e];
+  const int nrows = offsets[e + 1] - r0;
+  const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
+  const int koff = 16 * (lane >> 4);
+  const uint16_t* xr[kDecodeMaxRowBlocks];
 #pragma unroll
   for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
     const int row = rb * 16 + (lane & 15);
-    tok[rb] = (rb < nrb && row < nrows) ? sorted_token[r0 + row] : -1;
+    const int tok = sorted_token[r0 + min(row, nrows - 1)];
+    xr[rb] = row < nrows ? x + (size_t)tok * D + koff : nullptr;
   }
   floatx4 ag[kDecodeMaxRowBlocks], au[kDecodeMaxRowBlocks];
 #pragma unroll
@@ -126,35 +147,44 @@ __global__ __launch_bounds__(256) void k_gateup_decode(int D, int I, int E, cons
     ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
     au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  const int c0 = (KC * wv) >> 2, c1 = (KC * (wv + 1)) >> 2;
-  const int koff = 16 * (lane >> 4);
-  for (int c = c0; c < c1; ++c) {
-    const uint4 qg = *reinterpret_cast<const uint4*>(bg + (size_t)c * 1024 + lane * 16);
-    const uint4 qu = *reinterpret_cast<const uint4*>(bu + (size_t)c * 1024 + lane * 16);
-    bf16x8 bg0, bg1, bu0, bu1;
-    dequant16(qg, sg, bg0, bg1);
-    dequant16(qu, su, bu0, bu1);
+  for (int cb = c0; cb < c1; cb += NB) {
+    if (cb != c0) load_w(cb);
 #pragma unroll
     for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
       if (rb < nrb) {
-        uint4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
-        if (tok[rb] >= 0) {
-          const uint4* ap = reinterpret_cast<const uint4*>(x + (size_t)tok[rb] * D + c * 64 + koff);
-          a0 = ap[0];
-          a1 = ap[1];
+        uint4 a0[NB], a1[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          a0[i] = uint4{0, 0, 0, 0};
+          a1[i] = uint4{0, 0, 0, 0};
+          if (xr[rb] && (!GUARD || cb + i < c1)) {
+            const uint4* ap = reinterpret_cast<const uint4*>(xr[rb] + (cb + i) * 64);
+            a0[i] = ap[0];
+            a1[i] = ap[1];
+          }
         }
-        ag[rb] = mfma16(as_bf16x8(a0), bg0, ag[rb]);
-        ag[rb] = mfma16(as_bf16x8(a1), bg1, ag[rb]);
-        au[rb] = mfma16(as_bf16x8(a0), bu0, au[rb]);
-        au[rb] = mfma16(as_bf16x8(a1), bu1, au[rb]);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          if (!GUARD || cb + i < c1) {
+            bf16x8 bg0, bg1, bu0, bu1;
+            dequant16(qg[i], sg, bg0, bg1);
+            dequant16(qu[i], su, bu0, bu1);
+            ag[rb] = mfma16(as_bf16x8(a0[i]), bg0, ag[rb]);
+            ag[rb] = mfma16(as_bf16x8(a1[i]), bg1, ag[rb]);
+            au[rb] = mfma16(as_bf16x8(a0[i]), bu0, au[rb]);
+            au[rb] = mfma16(as_bf16x8(a1[i]), bu1, au[rb]);
+          }
+        }
       }
     }
   }
   if (wv > 0) {
 #pragma unroll
     for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
-      red[wv - 1][rb][0][lane] = ag[rb];
-      red[wv - 1][rb][1][lane] = au[rb];
+      if (rb < nrb) {
+        red[wv - 1][rb][0][lane] = ag[rb];
+        red[wv - 1][rb][1][lane] = au[rb];
+      }
     }
   }
   __syncthreads();
@@ -164,7 +194,7 @@ __global__ __launch_bounds__(256) void k_gateup_decode(int D, int I, int E, cons
     if (rb >= nrb) break;
     floatx4 g = ag[rb], u = au[rb];
 #pragma unroll
-    for (int w = 0; w < 3; ++w) {
+    for (int w = 0; w < WPB - 1; ++w) {
       g += red[w][rb][0][lane];
       u += red[w][rb][1][lane];
     }
@@ -179,59 +209,80 @@ __global__ __launch_bounds__(256) void k_gateup_decode(int D, int I, int E, cons
   }
 }
 
-template <int NCG>
-__global__ __launch_bounds__(256) void k_down_decode(int D, int I, int E, const uint16_t* __restrict__ h_sorted,
+// Down projection for decode: one block per (active expert, NCG*16 output
+// columns), the reduction axis (I) split over the four waves; same load order
+// as the gate/up kernel.
+template <int WPB, int NCG, int NB, bool GUARD>
+__global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const uint16_t* __restrict__ h_sorted,
                                                       const int32_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ active,
                                                       const int8_t* __restrict__ w2, const float* __restrict__ s2,
                                                       uint16_t* __restrict__ y_sorted) {
-  __shared__ floatx4 red[3][kDecodeMaxRowBlocks][NCG][64];
+  __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][kDecodeMaxRowBlocks][NCG][64];
   const int dt = blockIdx.x;  // NCG*16 output columns
   const int slot = blockIdx.y;
-  if (slot >= active[E]) return;
-  const int e = active[slot];
-  const int r0 = offsets[e];
-  const int nrows = offsets[e + 1] - r0;
-  const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
+  const int n_active = active[E];
+  const int e = active[slot < E ? slot : 0];
+  if (slot >= n_active) return;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int DG = D >> 4, KC = I >> 6;
   const size_t cell = (size_t)(I >> 4) * 256;
-  float sc[NCG];
-  const int8_t* bp[NCG];
+  const int8_t* bp = w2 + ((size_t)e * DG + dt * NCG) * cell + lane * 16;
+  const int c0 = (KC * wv) / WPB, c1 = (KC * (wv + 1)) / WPB;
+  uint4 q[NB][NCG];
+  auto load_w = [&](int cb) {
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) {
-    const int dg = dt * NCG + cg;
-    bp[cg] = w2 + ((size_t)e * DG + dg) * cell;
-    sc[cg] = s2[(size_t)e * D + dg * 16 + (lane & 15)];
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg)
+        if (!GUARD || cb + i < c1) q[i][cg] = *reinterpret_cast<const uint4*>(bp + cg * cell + (size_t)(cb + i) * 1024);
+  };
+  load_w(c0);
+  float sc[NCG];
+#pragma unroll
+  for (int cg = 0; cg < NCG; ++cg) sc[cg] = s2[(size_t)e * D + (dt * NCG + cg) * 16 + (lane & 15)];
+  const int r0 = offsets[e];
+  const int nrows = offsets[e + 1] - r0;
+  const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
+  const int koff = 16 * (lane >> 4);
+  const uint16_t* hr[kDecodeMaxRowBlocks];
+#pragma unroll
+  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+    const int row = rb * 16 + (lane & 15);
+    hr[rb] = row < nrows ? h_sorted + (size_t)(r0 + row) * I + koff : nullptr;
   }
   floatx4 acc[kDecodeMaxRowBlocks][NCG];
 #pragma unroll
   for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb)
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) acc[rb][cg] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int c0 = (KC * wv) >> 2, c1 = (KC * (wv + 1)) >> 2;
-  const int koff = 16 * (lane >> 4);
-  for (int c = c0; c < c1; ++c) {
-    bf16x8 b0[NCG], b1[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const uint4 q = *reinterpret_cast<const uint4*>(bp[cg] + (size_t)c * 1024 + lane * 16);
-      dequant16(q, sc[cg], b0[cg], b1[cg]);
-    }
+  for (int cb = c0; cb < c1; cb += NB) {
+    if (cb != c0) load_w(cb);
 #pragma unroll
     for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
       if (rb < nrb) {
-        const int row = rb * 16 + (lane & 15);
-        uint4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
-        if (row < nrows) {
-          const uint4* ap = reinterpret_cast<const uint4*>(h_sorted + (size_t)(r0 + row) * I + c * 64 + koff);
-          a0 = ap[0];
-          a1 = ap[1];
+        uint4 a0[NB], a1[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          a0[i] = uint4{0, 0, 0, 0};
+          a1[i] = uint4{0, 0, 0, 0};
+          if (hr[rb] && (!GUARD || cb + i < c1)) {
+            const uint4* ap = reinterpret_cast<const uint4*>(hr[rb] + (cb + i) * 64);
+            a0[i] = ap[0];
+            a1[i] = ap[1];
+          }
         }
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) {
-          acc[rb][cg] = mfma16(as_bf16x8(a0), b0[cg], acc[rb][cg]);
-          acc[rb][cg] = mfma16(as_bf16x8(a1), b1[cg], acc[rb][cg]);
+        for (int i = 0; i < NB; ++i) {
+          if (!GUARD || cb + i < c1) {
+#pragma unroll
+            for (int cg = 0; cg < NCG; ++cg) {
+              bf16x8 b0, b1;
+              dequant16(q[i][cg], sc[cg], b0, b1);
+              acc[rb][cg] = mfma16(as_bf16x8(a0[i]), b0, acc[rb][cg]);
+              acc[rb][cg] = mfma16(as_bf16x8(a1[i]), b1, acc[rb][cg]);
+            }
+          }
         }
       }
     }
@@ -239,8 +290,9 @@ __global__ __launch_bounds__(256) void k_down_decode(int D, int I, int E, const 
   if (wv > 0) {
 #pragma unroll
     for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb)
+      if (rb < nrb)
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) red[wv - 1][rb][cg][lane] = acc[rb][cg];
+        for (int cg = 0; cg < NCG; ++cg) red[wv - 1][rb][cg][lane] = acc[rb][cg];
   }
   __syncthreads();
   if (wv != 0) return;
@@ -251,7 +303,7 @@ __global__ __launch_bounds__(256) void k_down_decode(int D, int I, int E, const 
     for (int cg = 0; cg < NCG; ++cg) {
       floatx4 v = acc[rb][cg];
 #pragma unroll
-      for (int w = 0; w < 3; ++w) v += red[w][rb][cg][lane];
+      for (int w = 0; w < WPB - 1; ++w) v += red[w][rb][cg][lane];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int row = rb * 16 + 4 * (lane >> 4) + j;
@@ -490,28 +542,86 @@ __global__ __launch_bounds__(256) void k_down_generic(int D, int I, const A* __r
 // ---------------------------------------------------------------------------
 // Combine: out[t, n] = round(sum_{j<K} w[t,j] * y_sorted[inv[t*K+j], n]),
 // sequential fmaf over j from +0.0f; no atomics, one writer per element.
+// A thread owns 8 consecutive columns (one 16-byte bf16 load per row); the
+// row indices and weights of a token are read first and the K row loads are
+// issued in batches of 8 before the FMAs.
 // ---------------------------------------------------------------------------
-template <typename A, int VEC>
-__global__ __launch_bounds__(256) void k_combine(int T, int K, int D, const A* __restrict__ y,
-                                                  const int32_t* __restrict__ inv, const float* __restrict__ w,
-                                                  A* __restrict__ out) {
-  const int t = blockIdx.y;
-  const int n0 = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
-  if (n0 >= D) return;
-  float acc[VEC];
+template <typename A>
+struct Vec8;
+template <>
+struct Vec8<uint16_t> {
+  __device__ __forceinline__ static void load(const uint16_t* p, float* v) {
+    const uint4 q = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-  for (int j = 0; j < K; ++j) {
-    const float wj = w[(int64_t)t * K + j];
-    const A* yr = y + (int64_t)inv[(int64_t)t * K + j] * D;
-#pragma unroll
-    for (int v = 0; v < VEC; ++v)
-      if (VEC == 1 || n0 + v < D) acc[v] = __builtin_fmaf(wj, Act<A>::load(yr, n0 + v), acc[v]);
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = __uint_as_float(w[j] << 16);
+      v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
   }
+  __device__ __forceinline__ static void store(uint16_t* p, const float* v) {
+    uint32_t w[4];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v)
-    if (VEC == 1 || n0 + v < D) Act<A>::store(out, (int64_t)t * D + n0 + v, acc[v]);
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)f32_to_bf16_bits(v[2 * j]) | ((uint32_t)f32_to_bf16_bits(v[2 * j + 1]) << 16);
+    *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+  }
+};
+template <>
+struct Vec8<float> {
+  __device__ __forceinline__ static void load(const float* p, float* v) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  }
+  __device__ __forceinline__ static void store(float* p, const float* v) {
+    reinterpret_cast<float4*>(p)[0] = float4{v[0], v[1], v[2], v[3]};
+    reinterpret_cast<float4*>(p)[1] = float4{v[4], v[5], v[6], v[7]};
+  }
+};
+
+template <typename A>
+__global__ __launch_bounds__(256) void k_combine8(int T, int K, int D, const A* __restrict__ y,
+                                                   const int32_t* __restrict__ inv, const float* __restrict__ w,
+                                                   A* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int n0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (n0 >= D) return;
+  float acc[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) acc[v] = 0.0f;
+  for (int jb = 0; jb < K; jb += 8) {
+    const int nj = min(8, K - jb);
+    float wj[8], yv[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < nj) {
+        wj[j] = w[(int64_t)t * K + jb + j];
+        Vec8<A>::load(y + (int64_t)inv[(int64_t)t * K + jb + j] * D + n0, yv[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < nj)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) acc[v] = __builtin_fmaf(wj[j], yv[j][v], acc[v]);
+  }
+  Vec8<A>::store(out + (int64_t)t * D + n0, acc);
 }
+
+// Any D: one column per thread.
+template <typename A>
+__global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* __restrict__ y,
+                                                   const int32_t* __restrict__ inv, const float* __restrict__ w,
+                                                   A* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= D) return;
+  float acc = 0.0f;
+  for (int j = 0; j < K; ++j)
+    acc = __builtin_fmaf(w[(int64_t)t * K + j], Act<A>::load(y, (int64_t)inv[(int64_t)t * K + j] * D + n), acc);
+  Act<A>::store(out, (int64_t)t * D + n, acc);
+}
+
 
 template <typename A>
 __global__ __launch_bounds__(256) void k_cast_from_f32(int64_t n, const float* __restrict__ in, A* __restrict__ out) {
@@ -540,15 +650,29 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
   const float* s13 = reinterpret_cast<const float*>(p.s13);
   const float* s2 = reinterpret_cast<const float*>(p.s2);
   if (decode) {
+    // shapes from a sweep on MI355X (30B-A3B layer, T = 1..64): four waves split
+    // the reduction, batches of 4 (gate/up) or 3 (down) chunks per load stage
     if (stages & kStageGateUp) {
-      hipLaunchKernelGGL(k_gateup_decode, dim3(I / 16, slots), dim3(256), 0, st, D, I, E, xb, offsets, active,
-                         sorted_token, w13, s13, hb);
+      const int cpw = (D / 64) / 4;  // chunks per wave
+      const dim3 grid(I / 16, slots);
+      if ((D / 64) % 4 == 0 && cpw % 4 == 0)
+        hipLaunchKernelGGL((k_gateup_decode<4, 4, false>), grid, dim3(256), 0, st, D, I, E, xb, offsets, active,
+                           sorted_token, w13, s13, hb);
+      else
+        hipLaunchKernelGGL((k_gateup_decode<4, 4, true>), grid, dim3(256), 0, st, D, I, E, xb, offsets, active,
+                           sorted_token, w13, s13, hb);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
     }
     if (stages & kStageDown) {
-      hipLaunchKernelGGL((k_down_decode<2>), dim3(D / 32, slots), dim3(256), 0, st, D, I, E, hb, offsets, active,
-                         w2, s2, yb);
+      const int cpw = (I / 64) / 4;
+      const dim3 grid(D / 32, slots);
+      if ((I / 64) % 4 == 0 && cpw % 3 == 0)
+        hipLaunchKernelGGL((k_down_decode<4, 2, 3, false>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
+                           s2, yb);
+      else
+        hipLaunchKernelGGL((k_down_decode<4, 2, 4, true>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
+                           s2, yb);
       return hipGetLastError();
     }
     return hipSuccess;
@@ -618,16 +742,23 @@ hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, 
 hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
                           hipStream_t st) {
   const int T = (int)d.tokens, D = (int)d.hidden, K = (int)d.top_k;
-  if (d.act_dtype == KMOE_DTYPE_BF16) {
-    if (D % 8 == 0)
-      hipLaunchKernelGGL((k_combine<uint16_t, 8>), dim3((D / 8 + 255) / 256, T), dim3(256), 0, st, T, K, D,
+  const bool bf16 = d.act_dtype == KMOE_DTYPE_BF16;
+  if (D % 8 == 0) {
+    const dim3 grid((D / 8 + 255) / 256, T);
+    if (bf16)
+      hipLaunchKernelGGL((k_combine8<uint16_t>), grid, dim3(256), 0, st, T, K, D,
                          reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out));
     else
-      hipLaunchKernelGGL((k_combine<uint16_t, 1>), dim3((D + 255) / 256, T), dim3(256), 0, st, T, K, D,
-                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out));
+      hipLaunchKernelGGL((k_combine8<float>), grid, dim3(256), 0, st, T, K, D, reinterpret_cast<const float*>(y_sorted),
+                         inv, topk_w, reinterpret_cast<float*>(out));
   } else {
-    hipLaunchKernelGGL((k_combine<float, 1>), dim3((D + 255) / 256, T), dim3(256), 0, st, T, K, D,
-                       reinterpret_cast<const float*>(y_sorted), inv, topk_w, reinterpret_cast<float*>(out));
+    const dim3 grid((D + 255) / 256, T);
+    if (bf16)
+      hipLaunchKernelGGL((k_combine1<uint16_t>), grid, dim3(256), 0, st, T, K, D,
+                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out));
+    else
+      hipLaunchKernelGGL((k_combine1<float>), grid, dim3(256), 0, st, T, K, D, reinterpret_cast<const float*>(y_sorted),
+                         inv, topk_w, reinterpret_cast<float*>(out));
   }
   return hipGetLastError();
 }

@@ -4,68 +4,57 @@
 // _moe_ragged (kappa/qwen3/ffn_moe.py:189-200, 212).
 #include <float.h>
 
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 
 namespace kmoe {
 
 // ---------------------------------------------------------------------------
-// Router logits in the canonical order.
-//
-// logits[t,e] = tree_s( fmaf-chain_{d in slice s}( x[t,d] * r[d,e] ) ),
-// slices of 64 hidden indices; the tree is p[i] += p[i+st] for st = 1,2,4,..
-// over the slices zero-padded to GW = next power of two.
-//
-// A group of GW lanes owns one slice each and TB tokens x 8 experts of output;
-// the slice tree is a shuffle-down reduction inside the group. x for the TB
-// tokens is staged in LDS as f32 with each 64-slice padded to 65 floats so the
-// lanes of a group (one slice each) hit distinct banks.
+// Router weight rows. A lane owns EPL (8 or 16) consecutive experts of one
+// hidden row and loads them with one or two 16-byte loads (8 bytes for an
+// int8 router with EPL = 8); LPR = E / EPL lanes cover a row contiguously.
 // ---------------------------------------------------------------------------
-template <int RT>
-struct RouterRow;
-
-// f32 router
-template <>
-struct RouterRow<0> {
-  __device__ __forceinline__ static void load8(const void* rw, int64_t off, float* r, const float*) {
-    const float* p = reinterpret_cast<const float*>(rw) + off;
+template <int RT, int EPL>
+struct RouterRow {
+  static constexpr int kBytes = EPL * (RT == 0 ? 4 : (RT == 1 ? 2 : 1));
+  static constexpr int kWords = kBytes / 4;
+  struct Raw {
+    uint32_t w[kWords];
+  };
+  __device__ __forceinline__ static void load(const void* rw, int64_t elem, Raw& r) {
+    const char* p = reinterpret_cast<const char*>(rw) + elem * (kBytes / EPL);
+    if constexpr (kWords % 4 == 0) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = p[j];
-  }
-  __device__ __forceinline__ static float load1(const void* rw, int64_t off, float) {
-    return reinterpret_cast<const float*>(rw)[off];
-  }
-};
-// bf16 router
-template <>
-struct RouterRow<1> {
-  __device__ __forceinline__ static void load8(const void* rw, int64_t off, float* r, const float*) {
-    const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(rw) + off);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      r[2 * j] = __uint_as_float(w[j] << 16);
-      r[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      for (int q = 0; q < kWords / 4; ++q) {
+        const uint4 v = reinterpret_cast<const uint4*>(p)[q];
+        r.w[4 * q] = v.x, r.w[4 * q + 1] = v.y, r.w[4 * q + 2] = v.z, r.w[4 * q + 3] = v.w;
+      }
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      r.w[0] = v.x, r.w[1] = v.y;
     }
   }
-  __device__ __forceinline__ static float load1(const void* rw, int64_t off, float) {
-    return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(rw)[off]);
-  }
-};
-// int8 router: f32(q) * f32(scale[e])  (to_compute_dtype(router_w, f32))
-template <>
-struct RouterRow<2> {
-  __device__ __forceinline__ static void load8(const void* rw, int64_t off, float* r, const float* s) {
-    const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const int8_t*>(rw) + off);
-    const uint32_t w[2] = {v.x, v.y};
+  // to_compute_dtype(router_w, f32) (kappa/qwen3/quant.py:34-38): int8 is f32(q) * f32(scale)
+  __device__ __forceinline__ static void convert(const Raw& r, const float* sc, float* out) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int8_t q = (int8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
-      r[j] = (float)q * s[j];
+    for (int i = 0; i < EPL; ++i) {
+      if constexpr (RT == 0) {
+        out[i] = __uint_as_float(r.w[i]);
+      } else if constexpr (RT == 1) {
+        const uint32_t v = r.w[i >> 1];
+        out[i] = __uint_as_float((i & 1) ? (v & 0xffff0000u) : (v << 16));
+      } else {
+        const int8_t q = (int8_t)((r.w[i >> 2] >> (8 * (i & 3))) & 0xffu);
+        out[i] = (float)q * sc[i];
+      }
     }
   }
-  __device__ __forceinline__ static float load1(const void* rw, int64_t off, float s) {
-    return (float)reinterpret_cast<const int8_t*>(rw)[off] * s;
+  __device__ __forceinline__ static float load1(const void* rw, int64_t elem, float sc) {
+    if constexpr (RT == 0) return reinterpret_cast<const float*>(rw)[elem];
+    if constexpr (RT == 1) return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(rw)[elem]);
+    return (float)reinterpret_cast<const int8_t*>(rw)[elem] * sc;
   }
 };
 
@@ -74,120 +63,186 @@ __device__ __forceinline__ float load_scale(const void* scale, int scale_bf16, i
                     : reinterpret_cast<const float*>(scale)[i];
 }
 
-template <typename A, int RT, int TB, bool VEC>
-__global__ __launch_bounds__(256) void k_router_logits(int T, int D, int E, const A* __restrict__ x,
-                                                        const void* __restrict__ rw, const void* __restrict__ rscale,
-                                                        int scale_bf16, int scale_per_channel,
-                                                        float* __restrict__ logits, int gw_log2) {
-  extern __shared__ float xs[];  // [TB][S][65]
+// ---------------------------------------------------------------------------
+// Fused router: logits in the canonical order, top-k, softmax.
+//
+// logits[t,e] = tree_s( fmaf-chain_{d in slice s}( x[t,d] * r[d,e] ) ) with
+// slices of 64 hidden indices and the pairwise tree p[i] += p[i+st],
+// st = 1, 2, 4, ... over the slices zero-padded to P = next power of two.
+//
+// Slice s is owned by lane group lg = s % SPW of wave-group s / SPW (a lane
+// group is LPR lanes covering all experts; SPW groups per wave). A wave runs
+// G wave-groups one after the other; the tree levels st < SPW are shuffles
+// between lane groups, the levels SPW <= st < SPW*G combine the G wave-groups
+// in registers, and the remaining levels combine the waves' partials through
+// LDS. x for the TB tokens of the block is staged in LDS as f32
+// [slice][64][TB] (slice pitch padded by 4 floats: the lane groups of a wave
+// read different slices in distinct banks); the same LDS then holds the wave
+// partials [wave][TB][E].
+//
+// Then one wave per token selects the top K (value descending, ties to the
+// lower expert index; NaN ranks as -inf) with K wave-wide arg-max rounds, and
+// lane j < K writes selection j and its softmax weight
+//   w_j = expf(l_j - l_0) / sum_{i<K} expf(l_i - l_0)   (sum in i order),
+// rounded to the activation dtype when out_bf16.
+// ---------------------------------------------------------------------------
+template <int TB, int EPL>
+struct Acc {
+  float v[TB][EPL];
+};
+
+template <typename A, int RT, int EPL, int TB, int G>
+__global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int LPR, int SPW, int P,
+                                                 const A* __restrict__ x, const void* __restrict__ rw,
+                                                 const void* __restrict__ rscale, int scale_bf16, int scale_pc,
+                                                 float* __restrict__ logits, int32_t* __restrict__ topk_idx,
+                                                 float* __restrict__ topk_w, int out_bf16) {
+  using Row = RouterRow<RT, EPL>;
+  // rows per prefetch stage: two stages of raw rows stay within 32 registers
+  constexpr int U0 = 16 / Row::kWords < 1 ? 1 : 16 / Row::kWords;
+  constexpr int U = U0 < 16 / TB ? U0 : 16 / TB;
+  extern __shared__ float lds[];
+  const int NWB = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int S = (D + kRouterSlice - 1) / kRouterSlice;
-  const int GW = 1 << gw_log2;
+  const int XP = kRouterSlice * TB + 4;
   const int t0 = blockIdx.x * TB;
-  const int xstride = S * 65;
-  for (int i = threadIdx.x; i < TB * D; i += blockDim.x) {
-    const int tt = i / D, d = i - tt * D;
-    const float v = (t0 + tt < T) ? Act<A>::load(x, (int64_t)(t0 + tt) * D + d) : 0.0f;
-    xs[tt * xstride + (d >> 6) * 65 + (d & 63)] = v;
-  }
-  __syncthreads();
-
-  const int ls = threadIdx.x & (GW - 1);
-  const int g = threadIdx.x >> gw_log2;
-  const int NG = (int)blockDim.x >> gw_log2;
-  const int e0 = (blockIdx.y * NG + g) * 8;
-
-  float sc[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    sc[j] = 0.0f;
-    if (RT == 2 && e0 + j < E) sc[j] = load_scale(rscale, scale_bf16, scale_per_channel ? e0 + j : 0);
-  }
-
-  float acc[TB][8];
 #pragma unroll
   for (int tt = 0; tt < TB; ++tt)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[tt][j] = 0.0f;
+    for (int d = threadIdx.x; d < D; d += blockDim.x)
+      lds[(d >> 6) * XP + (d & 63) * TB + tt] = (t0 + tt < T) ? Act<A>::load(x, (int64_t)(t0 + tt) * D + d) : 0.0f;
+  __syncthreads();
 
-  if (ls < S && e0 < E) {
-    const int d0 = ls * kRouterSlice;
-    const int d1 = min(D, d0 + kRouterSlice);
-    const float* xl = xs + ls * 65;
-    for (int d = d0; d < d1; ++d) {
-      float r[8];
-      if (VEC) {
-        RouterRow<RT>::load8(rw, (int64_t)d * E + e0, r, sc);
-      } else {
+  const int lg = lane / LPR, le = lane - lg * LPR;
+  const int e0 = le * EPL;
+  const bool lane_on = lg < SPW && e0 < E;
+  const bool vec = (E % 8) == 0 && e0 + EPL <= E;
+  float sc[EPL];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = (e0 + j < E) ? RouterRow<RT>::load1(rw, (int64_t)d * E + e0 + j, sc[j]) : 0.0f;
-      }
-#pragma unroll
-      for (int tt = 0; tt < TB; ++tt) {
-        const float xv = xl[tt * xstride + (d - d0)];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[tt][j] = __builtin_fmaf(xv, r[j], acc[tt][j]);
-      }
-    }
+  for (int i = 0; i < EPL; ++i) {
+    sc[i] = 0.0f;
+    if (RT == 2 && e0 + i < E) sc[i] = load_scale(rscale, scale_bf16, scale_pc ? e0 + i : 0);
   }
-  // pairwise tree over the slices held by the GW lanes of this group
-  for (int st = 1; st < GW; st <<= 1) {
+
+  Acc<TB, EPL> p0, p1;
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    Acc<TB, EPL> c;
 #pragma unroll
     for (int tt = 0; tt < TB; ++tt)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[tt][j] = acc[tt][j] + __shfl_down(acc[tt][j], st, GW);
-  }
-  if (ls == 0 && e0 < E) {
+      for (int i = 0; i < EPL; ++i) c.v[tt][i] = 0.0f;
+    const int s = (w * G + gi) * SPW + lg;
+    if (lane_on && s < S) {
+      const int d0 = s * kRouterSlice;
+      const int d1 = min(D, d0 + kRouterSlice);
+      const float* xs = lds + s * XP - d0 * TB;
+      if (vec && d1 - d0 == kRouterSlice) {
+        typename Row::Raw cur[U], nxt[U];
 #pragma unroll
-    for (int tt = 0; tt < TB; ++tt) {
-      if (t0 + tt >= T) break;
+        for (int u = 0; u < U; ++u) Row::load(rw, (int64_t)(d0 + u) * E + e0, nxt[u]);
+        for (int db = d0; db < d1; db += U) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (e0 + j < E) logits[(int64_t)(t0 + tt) * E + e0 + j] = acc[tt][j];
+          for (int u = 0; u < U; ++u) cur[u] = nxt[u];
+          if (db + U < d1) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) Row::load(rw, (int64_t)(db + U + u) * E + e0, nxt[u]);
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            float r[EPL], xv[TB];
+            Row::convert(cur[u], sc, r);
+#pragma unroll
+            for (int tt = 0; tt < TB; ++tt) xv[tt] = xs[(db + u) * TB + tt];
+#pragma unroll
+            for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+              for (int i = 0; i < EPL; ++i) c.v[tt][i] = __builtin_fmaf(xv[tt], r[i], c.v[tt][i]);
+          }
+        }
+      } else {
+        for (int d = d0; d < d1; ++d) {
+          float r[EPL];
+#pragma unroll
+          for (int i = 0; i < EPL; ++i) r[i] = (e0 + i < E) ? Row::load1(rw, (int64_t)d * E + e0 + i, sc[i]) : 0.0f;
+#pragma unroll
+          for (int tt = 0; tt < TB; ++tt) {
+            const float xv = xs[d * TB + tt];
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) c.v[tt][i] = __builtin_fmaf(xv, r[i], c.v[tt][i]);
+          }
+        }
+      }
     }
+    // tree levels st < SPW: lane group lg += lane group lg + st
+    for (int st = 1; st < SPW && st < P; st <<= 1) {
+#pragma unroll
+      for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) c.v[tt][i] = c.v[tt][i] + __shfl_down(c.v[tt][i], st * LPR, 64);
+    }
+    // tree levels over the wave's G wave-groups (G <= 4)
+#pragma unroll
+    for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) {
+        if (G == 1 || gi == 0) {
+          p0.v[tt][i] = c.v[tt][i];
+        } else if (gi == 1) {
+          p0.v[tt][i] = p0.v[tt][i] + c.v[tt][i];
+        } else if (gi == 2) {
+          p1.v[tt][i] = c.v[tt][i];
+        } else {
+          p1.v[tt][i] = p1.v[tt][i] + c.v[tt][i];
+          p0.v[tt][i] = p0.v[tt][i] + p1.v[tt][i];
+        }
+      }
   }
-}
-
-// ---------------------------------------------------------------------------
-// Top-k (value descending, ties to the lower expert index) and softmax over the
-// selected logits, rounded to the activation dtype; per 64-token block expert
-// histogram for the dispatch. One wave per token; 16 waves per block.
-// ---------------------------------------------------------------------------
-template <bool BF16W>
-__global__ __launch_bounds__(1024) void k_topk(int T, int E, int K, const float* __restrict__ logits,
-                                                int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
-                                                int32_t* __restrict__ hist) {
-  __shared__ int h[kMaxExperts];
-  __shared__ float sv[16][kMaxTopK];
-  __shared__ int si[16][kMaxTopK];
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int tb0 = blockIdx.x * kDispatchBlock;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) h[e] = 0;
+  __syncthreads();  // x no longer needed: the LDS now holds the wave partials
+  float* part = lds;
+  const int TE = TB * E;
+  if (lg == 0) {
+#pragma unroll
+    for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+      for (int i = 0; i < EPL; ++i)
+        if (e0 + i < E) part[(size_t)w * TE + tt * E + e0 + i] = p0.v[tt][i];
+  }
   __syncthreads();
-  const int nper = (E + 63) / 64;
-  for (int tl = wv; tl < kDispatchBlock; tl += 16) {
-    const int t = tb0 + tl;
-    if (t >= T) break;
-    const float* lt = logits + (int64_t)t * E;
-    float v[kMaxExperts / 64];
-    uint32_t taken = 0;
-#pragma unroll
-    for (int i = 0; i < kMaxExperts / 64; ++i) {
-      const int e = lane + 64 * i;
-      const float lv = (i < nper && e < E) ? lt[e] : -INFINITY;
-      v[i] = (lv != lv) ? -INFINITY : lv;  // NaN ranks lowest, so a winner always exists
+  // the tree levels across waves, in place: part[g] += part[g + st]
+  for (int st = 1; st < NWB; st <<= 1) {
+    const int n = (NWB / (2 * st)) * TE;
+    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
+      const int g = (idx / TE) * 2 * st, rem = idx - (idx / TE) * TE;
+      part[(size_t)g * TE + rem] = part[(size_t)g * TE + rem] + part[(size_t)(g + st) * TE + rem];
     }
+    __syncthreads();
+  }
+
+  // top-k: lane owns experts lane + 64*i, i < EPL (E <= 64 * EPL)
+  for (int tt = w; tt < TB; tt += NWB) {
+    const int t = t0 + tt;
+    if (t >= T) break;
+    float v[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      const float q = e < E ? part[tt * E + e] : 0.0f;
+      v[i] = (e < E && q == q) ? q : -INFINITY;
+      if (logits && e < E) logits[(int64_t)t * E + e] = q;
+    }
+    uint32_t taken = 0;
+    float my_v = 0.0f;
+    int my_i = 0;
     for (int j = 0; j < K; ++j) {
       float bv = -INFINITY;
       int bi = 0x7fffffff;
 #pragma unroll
-      for (int i = 0; i < kMaxExperts / 64; ++i) {
+      for (int i = 0; i < EPL; ++i) {
         const int e = lane + 64 * i;
-        if (i < nper && e < E && !((taken >> i) & 1u)) {
-          if (v[i] > bv || (v[i] == bv && e < bi)) {
-            bv = v[i];
-            bi = e;
-          }
+        if (e < E && !((taken >> i) & 1u) && (v[i] > bv || bi == 0x7fffffff)) {
+          bv = v[i];
+          bi = e;
         }
       }
 #pragma unroll
@@ -200,103 +255,148 @@ __global__ __launch_bounds__(1024) void k_topk(int T, int E, int K, const float*
         }
       }
       if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-      if (lane == 0) {
-        sv[wv][j] = bv;
-        si[wv][j] = bi;
+      if (lane == j) {
+        my_v = bv;
+        my_i = bi;
       }
     }
-    __builtin_amdgcn_wave_barrier();
-    if (lane == 0) {
-      const float m = sv[wv][0];
-      float s = 0.0f;
-      for (int j = 0; j < K; ++j) s = s + expf(sv[wv][j] - m);
-      for (int j = 0; j < K; ++j) {
-        const float p = expf(sv[wv][j] - m) / s;
-        topk_w[(int64_t)t * K + j] = BF16W ? round_bf16(p) : p;
-        topk_idx[(int64_t)t * K + j] = si[wv][j];
-        atomicAdd(&h[si[wv][j]], 1);
-      }
+    const float m = __shfl(my_v, 0, 64);
+    const float ej = expf(my_v - m);
+    float ssum = 0.0f;
+    for (int j = 0; j < K; ++j) ssum = ssum + __shfl(ej, j, 64);
+    if (lane < K) {
+      const float p = ej / ssum;
+      topk_w[(int64_t)t * K + lane] = out_bf16 ? round_bf16(p) : p;
+      topk_idx[(int64_t)t * K + lane] = my_i;
     }
-    __builtin_amdgcn_wave_barrier();
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[(int64_t)blockIdx.x * E + e] = h[e];
 }
 
 // ---------------------------------------------------------------------------
-// Dispatch: stable counting sort of the row-major (t, j) assignments by
-// expert. Block b owns tokens [64b, 64b+64); its write cursor for expert e is
-// offsets[e] + sum_{b' < b} hist[b'][e]; within the block tokens are taken in
-// increasing order, which keeps the sort stable (jnp.argsort(stable=True)).
+// Dispatch: stable counting sort of the row-major (t, j) assignments by expert
+// (jnp.argsort(stable=True) over the flattened top-k indices).
+//
+// Tokens are cut into chunks of 64. Within a chunk, the assignments of expert
+// e form a 64-bit token mask (a token picks an expert at most once), so the
+// stable rank of token tl among them is popcount(mask[e] & ((1 << tl) - 1)).
+// The position of an assignment is
+//   offsets[e] + (assignments of e in earlier chunks) + rank,
+// with the per-chunk counts from k_dispatch_count.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_dispatch(int T, int E, int K, int nblk, const int32_t* __restrict__ topk_idx,
-                                                   const int32_t* __restrict__ hist, int32_t* __restrict__ group_sizes,
-                                                   int32_t* __restrict__ offsets, int32_t* __restrict__ active,
-                                                   int32_t* __restrict__ sorted_token,
-                                                   int32_t* __restrict__ sorted_expert, int32_t* __restrict__ inv) {
-  __shared__ int tot[kMaxExperts];
-  __shared__ int cur[kMaxExperts];
+__device__ __forceinline__ void chunk_masks(int T, int E, int K, int b, const int32_t* __restrict__ topk_idx,
+                                            unsigned long long* mask) {
+  for (int e = threadIdx.x; e < E; e += blockDim.x) mask[e] = 0ull;
+  __syncthreads();
+  const int t0 = b * kDispatchBlock;
+  const int n = min(kDispatchBlock, T - t0) * K;
+  for (int m = threadIdx.x; m < n; m += blockDim.x) {
+    const int tl = m / K;
+    const int e = topk_idx[(int64_t)t0 * K + m];
+    if ((unsigned)e < (unsigned)E) atomicOr(&mask[e], 1ull << tl);
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void k_dispatch_count(int T, int E, int K, const int32_t* __restrict__ topk_idx,
+                                                         int32_t* __restrict__ hist) {
+  __shared__ unsigned long long mask[kMaxExperts];
+  chunk_masks(T, E, K, blockIdx.x, topk_idx, mask);
+  for (int e = threadIdx.x; e < E; e += blockDim.x) hist[(int64_t)blockIdx.x * E + e] = __popcll(mask[e]);
+}
+
+// hist == nullptr: counts come from this block's masks (valid when T <= 64).
+__global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, int nblk,
+                                                           const int32_t* __restrict__ topk_idx,
+                                                           const int32_t* __restrict__ hist,
+                                                           int32_t* __restrict__ group_sizes,
+                                                           int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+                                                           int32_t* __restrict__ sorted_token,
+                                                           int32_t* __restrict__ sorted_expert,
+                                                           int32_t* __restrict__ inv) {
+  __shared__ unsigned long long mask[kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int wsum[4], wact[4];
   const int b = blockIdx.x;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int before = 0, after = 0;
-    for (int bb = 0; bb < b; ++bb) before += hist[(int64_t)bb * E + e];
-    for (int bb = b; bb < nblk; ++bb) after += hist[(int64_t)bb * E + e];
-    tot[e] = before + after;
-    cur[e] = before;
-  }
-  __syncthreads();
-  int pre_reg[kMaxExperts / 256];
-  int act_reg[kMaxExperts / 256];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  chunk_masks(T, E, K, b, topk_idx, mask);
+
+  // this thread's experts: 4*tid .. 4*tid+3
+  int tot[4], bef[4];
+  int lsum = 0, lact = 0;
 #pragma unroll
-  for (int i = 0; i < kMaxExperts / 256; ++i) {
-    const int e = threadIdx.x + 256 * i;
-    int s = 0, a = 0;
-    if (e < E)
-      for (int ee = 0; ee < e; ++ee) {
-        s += tot[ee];
-        a += tot[ee] > 0;
-      }
-    pre_reg[i] = s;
-    act_reg[i] = a;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kMaxExperts / 256; ++i) {
-    const int e = threadIdx.x + 256 * i;
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * tid + i;
+    tot[i] = 0;
+    bef[i] = 0;
     if (e < E) {
-      if (b == 0) {
-        group_sizes[e] = tot[e];
-        offsets[e] = pre_reg[i];
-        if (tot[e] > 0) active[act_reg[i]] = e;
-        if (e == E - 1) {
-          offsets[E] = pre_reg[i] + tot[e];
-          active[E] = act_reg[i] + (tot[e] > 0);
+      if (hist) {
+        for (int bb = 0; bb < nblk; ++bb) {
+          const int h = hist[(int64_t)bb * E + e];
+          tot[i] += h;
+          bef[i] += bb < b ? h : 0;
         }
+      } else {
+        tot[i] = __popcll(mask[e]);
       }
-      cur[e] += pre_reg[i];
+    }
+    lsum += tot[i];
+    lact += tot[i] > 0;
+  }
+  int isum = lsum, iact = lact;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int vs = __shfl_up(isum, off, 64);
+    const int va = __shfl_up(iact, off, 64);
+    if (lane >= off) {
+      isum += vs;
+      iact += va;
     }
   }
+  if (lane == 63) {
+    wsum[wv] = isum;
+    wact[wv] = iact;
+  }
   __syncthreads();
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    const int t1 = min(T, (b + 1) * kDispatchBlock);
-    for (int t = b * kDispatchBlock; t < t1; ++t) {
-      if (lane < K) {
-        const int m = t * K + lane;
-        const int e = topk_idx[m];
-        // indices outside [0, E) or a histogram that disagrees with them are
-        // caller errors; they are skipped rather than written out of bounds
-        if ((unsigned)e < (unsigned)E) {
-          const int p = cur[e];
-          cur[e] = p + 1;
-          if ((unsigned)p < (unsigned)(T * K)) {
-            sorted_token[p] = t;
-            sorted_expert[p] = e;
-            inv[m] = p;
-          }
-        }
+  int run = isum - lsum, arun = iact - lact;
+  for (int q = 0; q < wv; ++q) {
+    run += wsum[q];
+    arun += wact[q];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * tid + i;
+    if (e < E) {
+      if (b == 0) {
+        group_sizes[e] = tot[i];
+        offsets[e] = run;
+        if (tot[i] > 0) active[arun] = e;
       }
-      __builtin_amdgcn_wave_barrier();
+      base[e] = run + bef[i];
+    }
+    run += tot[i];
+    arun += tot[i] > 0;
+  }
+  if (b == 0 && tid == 255) {
+    offsets[E] = run;
+    active[E] = arun;
+  }
+  __syncthreads();
+
+  const int t0 = b * kDispatchBlock;
+  const int n = min(kDispatchBlock, T - t0) * K;
+  const int M = T * K;
+  for (int m = tid; m < n; m += blockDim.x) {
+    const int tl = m / K;
+    const int e = topk_idx[(int64_t)t0 * K + m];
+    // indices outside [0, E) or counts that disagree with them are caller errors
+    // of the stage entry point; they are skipped rather than written out of bounds
+    if ((unsigned)e < (unsigned)E) {
+      const int p = base[e] + __popcll(mask[e] & ((1ull << tl) - 1ull));
+      if ((unsigned)p < (unsigned)M) {
+        sorted_token[p] = t0 + tl;
+        sorted_expert[p] = e;
+        inv[(int64_t)t0 * K + m] = p;
+      }
     }
   }
 }
@@ -310,70 +410,101 @@ namespace kmoe_host {
 
 using namespace kmoe;
 
-template <typename A, int RT, int TB>
-static hipError_t launch_router_tb(const kmoe_desc& d, const void* x, const kmoe_weight& r, float* logits,
-                                   hipStream_t st) {
-  const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts;
-  const int S = (D + kRouterSlice - 1) / kRouterSlice;
-  int gw_log2 = 0;
-  while ((1 << gw_log2) < S) ++gw_log2;
-  const int NG = 256 >> gw_log2;
-  const int EB = NG * 8;
-  dim3 grid((T + TB - 1) / TB, (E + EB - 1) / EB);
-  const size_t lds = sizeof(float) * (size_t)TB * S * 65;
+struct RouteShape {
+  int S, P, EPL, LPR, SPW, G, NWB, TB;
+  size_t lds;
+};
+
+static RouteShape route_shape(const kmoe_desc& d) {
+  RouteShape r;
+  const int D = (int)d.hidden, E = (int)d.num_experts;
+  const int T = (int)d.tokens;
+  r.S = (D + kRouterSlice - 1) / kRouterSlice;
+  r.P = 1;
+  while (r.P < r.S) r.P <<= 1;
+  r.EPL = E <= 512 ? 8 : 16;
+  r.LPR = (E + r.EPL - 1) / r.EPL;
+  r.SPW = 1;
+  while (2 * r.SPW * r.LPR <= 64) r.SPW <<= 1;
+  const int NG = r.P > r.SPW ? r.P / r.SPW : 1;
+  r.G = NG > 16 ? NG / 16 : 1;
+  r.NWB = NG / r.G;
+  // tokens per block: accumulators within the register budget, x stage and
+  // partials <= 64 KB, and enough blocks to cover the chip
+  int tb = 8;
+  const int acc_cap = r.G > 1 ? 2 * r.EPL : 64;
+  auto x_bytes = [&](int t) { return (size_t)4 * r.S * (kRouterSlice * t + 4); };
+  while (tb > 1 && (tb * r.EPL > acc_cap || x_bytes(tb) > 65536 || (size_t)r.NWB * tb * E * 4 > 65536)) tb >>= 1;
+  while (tb > 1 && (T + tb - 1) / tb < 256) tb >>= 1;
+  r.TB = tb;
+  r.lds = std::max(x_bytes(tb), (size_t)4 * r.NWB * tb * E);
+  return r;
+}
+
+template <typename A, int RT, int EPL, int TB, int G>
+static void launch_route_k(const kmoe_desc& d, const RouteShape& rs, const void* x, const kmoe_weight& r,
+                           float* logits, int32_t* topk_idx, float* topk_w, hipStream_t st) {
+  const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts, K = (int)d.top_k;
   const int scale_bf16 = (r.dtype == KMOE_DTYPE_I8 && r.scale_dtype == KMOE_DTYPE_BF16) ? 1 : 0;
-  const int per_channel = (r.dtype == KMOE_DTYPE_I8 && r.scale_kind == KMOE_SCALE_CHANNEL) ? 1 : 0;
-  const bool vec = (E % 8) == 0;
-  if (vec)
-    hipLaunchKernelGGL((k_router_logits<A, RT, TB, true>), grid, dim3(256), lds, st, T, D, E,
-                       reinterpret_cast<const A*>(x), r.values, r.scale, scale_bf16, per_channel, logits, gw_log2);
-  else
-    hipLaunchKernelGGL((k_router_logits<A, RT, TB, false>), grid, dim3(256), lds, st, T, D, E,
-                       reinterpret_cast<const A*>(x), r.values, r.scale, scale_bf16, per_channel, logits, gw_log2);
-  return hipGetLastError();
+  const int scale_pc = (r.dtype == KMOE_DTYPE_I8 && r.scale_kind == KMOE_SCALE_CHANNEL) ? 1 : 0;
+  const int out_bf16 = d.act_dtype == KMOE_DTYPE_BF16 ? 1 : 0;
+  hipLaunchKernelGGL((k_route<A, RT, EPL, TB, G>), dim3((T + TB - 1) / TB), dim3(64 * rs.NWB), rs.lds, st, T, D, E,
+                     K, rs.LPR, rs.SPW, rs.P, reinterpret_cast<const A*>(x), r.values, r.scale, scale_bf16,
+                     scale_pc, logits, topk_idx, topk_w, out_bf16);
+}
+
+template <typename A, int RT, int EPL>
+static void route_tb(const kmoe_desc& d, const RouteShape& rs, const void* x, const kmoe_weight& r, float* logits,
+                     int32_t* idx, float* w, hipStream_t st) {
+  if (rs.G == 4) {
+    if (rs.TB == 2) return launch_route_k<A, RT, EPL, 2, 4>(d, rs, x, r, logits, idx, w, st);
+    return launch_route_k<A, RT, EPL, 1, 4>(d, rs, x, r, logits, idx, w, st);
+  }
+  if (rs.G == 2) {
+    if (rs.TB == 2) return launch_route_k<A, RT, EPL, 2, 2>(d, rs, x, r, logits, idx, w, st);
+    return launch_route_k<A, RT, EPL, 1, 2>(d, rs, x, r, logits, idx, w, st);
+  }
+  switch (rs.TB) {
+    case 8:
+      if constexpr (EPL == 8) return launch_route_k<A, RT, EPL, 8, 1>(d, rs, x, r, logits, idx, w, st);
+      [[fallthrough]];
+    case 4:
+      if constexpr (EPL == 8) return launch_route_k<A, RT, EPL, 4, 1>(d, rs, x, r, logits, idx, w, st);
+      [[fallthrough]];
+    case 2:
+      return launch_route_k<A, RT, EPL, 2, 1>(d, rs, x, r, logits, idx, w, st);
+    default:
+      return launch_route_k<A, RT, EPL, 1, 1>(d, rs, x, r, logits, idx, w, st);
+  }
 }
 
 template <typename A, int RT>
-static hipError_t launch_router_rt(const kmoe_desc& d, const void* x, const kmoe_weight& r, float* logits,
-                                   hipStream_t st) {
-  const int S = (int)((d.hidden + kRouterSlice - 1) / kRouterSlice);
-  // tokens per block: as many as the 64 KB x stage allows, fewer for small T
-  int tb = 8;
-  while (tb > 1 && (size_t)tb * S * 65 * sizeof(float) > 65536) tb >>= 1;
-  while (tb > 1 && d.tokens < (int64_t)tb * 16) tb >>= 1;
-  switch (tb) {
-    case 8:
-      return launch_router_tb<A, RT, 8>(d, x, r, logits, st);
-    case 4:
-      return launch_router_tb<A, RT, 4>(d, x, r, logits, st);
-    case 2:
-      return launch_router_tb<A, RT, 2>(d, x, r, logits, st);
-    default:
-      return launch_router_tb<A, RT, 1>(d, x, r, logits, st);
-  }
+static void route_epl(const kmoe_desc& d, const RouteShape& rs, const void* x, const kmoe_weight& r, float* logits,
+                      int32_t* idx, float* w, hipStream_t st) {
+  if (rs.EPL == 8) return route_tb<A, RT, 8>(d, rs, x, r, logits, idx, w, st);
+  return route_tb<A, RT, 16>(d, rs, x, r, logits, idx, w, st);
+}
+
+template <typename A>
+static void route_rt(const kmoe_desc& d, const RouteShape& rs, const void* x, const kmoe_weight& r, float* logits,
+                     int32_t* idx, float* w, hipStream_t st) {
+  if (r.dtype == KMOE_DTYPE_F32) return route_epl<A, 0>(d, rs, x, r, logits, idx, w, st);
+  if (r.dtype == KMOE_DTYPE_BF16) return route_epl<A, 1>(d, rs, x, r, logits, idx, w, st);
+  return route_epl<A, 2>(d, rs, x, r, logits, idx, w, st);
 }
 
 hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& r, float* logits, int32_t* topk_idx,
                         float* topk_w, int32_t* hist, hipStream_t st) {
-  hipError_t err;
-  const bool bf16 = d.act_dtype == KMOE_DTYPE_BF16;
-  const int rt = r.dtype == KMOE_DTYPE_F32 ? 0 : (r.dtype == KMOE_DTYPE_BF16 ? 1 : 2);
-  if (bf16) {
-    err = rt == 0 ? launch_router_rt<uint16_t, 0>(d, x, r, logits, st)
-                  : (rt == 1 ? launch_router_rt<uint16_t, 1>(d, x, r, logits, st)
-                             : launch_router_rt<uint16_t, 2>(d, x, r, logits, st));
-  } else {
-    err = rt == 0 ? launch_router_rt<float, 0>(d, x, r, logits, st)
-                  : (rt == 1 ? launch_router_rt<float, 1>(d, x, r, logits, st)
-                             : launch_router_rt<float, 2>(d, x, r, logits, st));
-  }
-  if (err != hipSuccess) return err;
+  const RouteShape rs = route_shape(d);
+  if (d.act_dtype == KMOE_DTYPE_BF16)
+    route_rt<uint16_t>(d, rs, x, r, logits, topk_idx, topk_w, st);
+  else
+    route_rt<float>(d, rs, x, r, logits, topk_idx, topk_w, st);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || !hist) return err;
   const int T = (int)d.tokens, E = (int)d.num_experts, K = (int)d.top_k;
   const int nblk = (T + kDispatchBlock - 1) / kDispatchBlock;
-  if (bf16)
-    hipLaunchKernelGGL((k_topk<true>), dim3(nblk), dim3(1024), 0, st, T, E, K, logits, topk_idx, topk_w, hist);
-  else
-    hipLaunchKernelGGL((k_topk<false>), dim3(nblk), dim3(1024), 0, st, T, E, K, logits, topk_idx, topk_w, hist);
+  hipLaunchKernelGGL(k_dispatch_count, dim3(nblk), dim3(256), 0, st, T, E, K, topk_idx, hist);
   return hipGetLastError();
 }
 
@@ -382,8 +513,9 @@ hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const in
                            int32_t* inv, hipStream_t st) {
   const int T = (int)d.tokens, E = (int)d.num_experts, K = (int)d.top_k;
   const int nblk = (T + kDispatchBlock - 1) / kDispatchBlock;
-  hipLaunchKernelGGL(k_dispatch, dim3(nblk), dim3(256), 0, st, T, E, K, nblk, topk_idx, hist, group_sizes, offsets,
-                     active, sorted_token, sorted_expert, inv);
+  if (!hist && nblk > 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_dispatch_scatter, dim3(nblk), dim3(256), 0, st, T, E, K, nblk, topk_idx, hist, group_sizes,
+                     offsets, active, sorted_token, sorted_expert, inv);
   return hipGetLastError();
 }
 
