@@ -325,8 +325,8 @@ constexpr int kBM = 128;
 constexpr int kAStride = 72;  // bf16 elements per LDS row (64 + 8 pad: conflict-free fragment reads)
 
 struct PrefillLds {
-  uint16_t a[2][kBM][kAStride];
-  uint16_t b[2][2][8][64][8];  // [buf][sub-step][col group][lane][8 bf16]
+  alignas(16) uint16_t a[2][kBM][kAStride];
+  alignas(16) uint16_t b[2][2][8][64][8];  // [buf][sub-step][col group][lane][8 bf16]
   int mtp[kMaxExperts + 1];
   int tok[kBM];
 };
@@ -472,6 +472,221 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
         for (int n = 0; n < 4; ++n) drow[nt * 128 + wn * 64 + n * 16 + (lane & 15)] = f32_to_bf16_bits(acc[mi][n][j]);
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill grouped GEMM: up to 256 rows x 256 columns per tile (gate/up: 128
+// gate + 128 up columns, i.e. 128 columns of h; down: 256 output columns),
+// 64-deep k chunks, four waves.
+//
+// A work item is (expert, chunk of up to 256 of its rows, column tile). Wave w
+// owns all rows x 64 columns (four 16-column groups; for gate/up two gate
+// groups and the matching two up groups, so the SwiGLU epilogue pairs
+// registers of one lane) in accumulator tiles of v_mfma_f32_16x16x32_bf16.
+//
+// Global data reaches LDS by direct loads (global_load_lds_dwordx4), three
+// chunks deep, so no registers are spent on prefetch: A (activation rows,
+// gathered by token for gate/up) as [row][8 x 16 B] with the 16-byte pieces
+// XOR-swizzled by row, and each wave's raw int8 B (its 1 KB cell chunks, in
+// the packed layout a lane's 16 bytes are one column's 16 k = one MFMA B
+// fragment). Each chunk: issue chunk c+2's loads, read the wave's raw B and
+// dequantise it to bf16(q * bf16(s)), run the MFMAs with A fragments read one
+// tile ahead, wait for chunk c+1's loads, barrier. The barrier is the bare
+// s_barrier with explicit counter waits: a workgroup fence would also wait
+// for the chunk c+2 loads.
+//
+// Rows past the expert's end are computed on a clamped copy of row 0 and
+// never stored; the tile body is instantiated for 4, 8, 12 or 16 row tiles.
+// Work items are ordered (expert, column tile, row chunk) and consecutive
+// items go to the same XCD, so the row chunks of one expert reuse its
+// weights in that XCD's L2.
+// ---------------------------------------------------------------------------
+constexpr int kGM = 256;  // rows per tile
+constexpr int kGStageA = kGM * 64;   // bf16 per A stage
+constexpr int kGStageB = 4 * 4 * 1024;  // bytes per B stage: 4 waves x 4 cells x 1 KB
+
+typedef __attribute__((address_space(1))) void gmem_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes per lane from global memory straight into LDS: lane l's data lands
+// at lds_base + 16 * l (lds_base is wave-uniform).
+__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((gmem_void*)g, (lds_void*)lds_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding), then a workgroup barrier.
+// The compiler-only fences keep LDS accesses on their side of the barrier.
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+  static_assert(N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// 16-byte piece p of row r of an A stage
+__device__ __forceinline__ int a_swz(int r, int p) { return r * 64 + ((p ^ (r & 7)) << 3); }
+
+template <bool GATEUP, int MT>
+__device__ __forceinline__ void gemm_tile(const int* tok, uint16_t* A0, uint16_t* A1, uint16_t* A2, int8_t* B0,
+                                          int8_t* B1, int8_t* B2, int D, int I, int e, int nt, int row0, int rows,
+                                          const uint16_t* __restrict__ src, const int8_t* __restrict__ wp,
+                                          const float* __restrict__ sp, uint16_t* __restrict__ dst) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int Kdim = GATEUP ? D : I;
+  const int Ndim = GATEUP ? I : D;
+  constexpr int AJ = MT / 2;  // A load instructions per wave per chunk (8 rows each)
+  // A: instruction j of wave w covers rows 8q .. 8q+7, q = w*AJ + j; lane -> (row, piece)
+  uint32_t aoff[AJ];  // element offsets into src (src holds < 2^32 elements)
+#pragma unroll
+  for (int j = 0; j < AJ; ++j) {
+    const int r = 8 * (wv * AJ + j) + (lane >> 3);
+    const int t = tok[r] >= 0 ? tok[r] : tok[0];
+    aoff[j] = (uint32_t)t * (uint32_t)Kdim + (((lane & 7) ^ (r & 7)) << 3);
+  }
+  // B: this wave's four 16-column cells
+  const int8_t* bp[4];
+  float sc[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    if (GATEUP) {
+      const int which = g >> 1;                   // 0: gate, 1: up
+      const int igl = nt * 8 + wv * 2 + (g & 1);  // 16-column group of h
+      const size_t cid = ((size_t)e * (I >> 4) + igl) * 2 + which;
+      bp[g] = wp + cid * (size_t)(D >> 4) * 256 + lane * 16;
+      sc[g] = sp[cid * 16 + (lane & 15)];
+    } else {
+      const int dg = nt * 16 + wv * 4 + g;
+      bp[g] = wp + ((size_t)e * (D >> 4) + dg) * (size_t)(I >> 4) * 256 + lane * 16;
+      sc[g] = sp[(size_t)e * D + dg * 16 + (lane & 15)];
+    }
+  }
+  const int KC = Kdim >> 6;
+  floatx4 acc[MT][4];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) acc[mi][g] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int kLoads = AJ + 4;  // direct loads per lane per chunk
+#define KMOE_DMA(c, AS, BS)                                                              \
+  {                                                                                      \
+    const int cc = (c);                                                                  \
+    _Pragma("unroll") for (int j = 0; j < AJ; ++j)                                       \
+        dma16(src + aoff[j] + cc * 64, AS + (wv * AJ + j) * 512);                        \
+    _Pragma("unroll") for (int g = 0; g < 4; ++g)                                        \
+        dma16(bp[g] + (size_t)cc * 1024, BS + (wv * 4 + g) * 1024);                      \
+  }
+#define KMOE_STEP(c, AS, BS, AN, BN)                                                                      \
+  {                                                                                                       \
+    KMOE_DMA(min((c) + 2, KC - 1), AN, BN)                                                                \
+    bf16x8 lo[4], hi[4];                                                                                  \
+    _Pragma("unroll") for (int g = 0; g < 4; ++g) {                                                       \
+      const uint4 q = *reinterpret_cast<const uint4*>(BS + (wv * 4 + g) * 1024 + lane * 16);             \
+      dequant16(q, sc[g], lo[g], hi[g]);                                                                  \
+    }                                                                                                     \
+    _Pragma("unroll") for (int st = 0; st < 2; ++st) {                                                    \
+      const int p = 2 * (lane >> 4) + st;                                                                 \
+      _Pragma("unroll") for (int mi = 0; mi < MT; ++mi) {                                                 \
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(AS + a_swz(mi * 16 + (lane & 15), p));         \
+        _Pragma("unroll") for (int g = 0; g < 4; ++g) acc[mi][g] = mfma16(a, st ? hi[g] : lo[g], acc[mi][g]); \
+      }                                                                                                   \
+    }                                                                                                     \
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);                                                    \
+    _Pragma("unroll") for (int i = 0; i < 2 * MT; ++i) {                                                  \
+      __builtin_amdgcn_sched_group_barrier(0x002, 160 / (2 * MT) + 1, 0);                                 \
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                                  \
+      if (i + 2 < 2 * MT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                              \
+    }                                                                                                     \
+    wait_barrier<kLoads>();                                                                               \
+  }
+
+  KMOE_DMA(0, A0, B0)
+  KMOE_DMA(min(1, KC - 1), A1, B1)
+  wait_barrier<kLoads>();
+  for (int c = 0; c < KC; c += 3) {
+    KMOE_STEP(c, A0, B0, A2, B2)
+    if (c + 1 < KC) KMOE_STEP(c + 1, A1, B1, A0, B0)
+    if (c + 2 < KC) KMOE_STEP(c + 2, A2, B2, A1, B1)
+  }
+#undef KMOE_STEP
+#undef KMOE_DMA
+
+  // epilogue: lane holds rows 4*(lane/16)+j of each 16x16 tile, column lane%16;
+  // one tile row at a time (the scheduling barrier keeps the accumulator reads
+  // from being hoisted all at once)
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = mi * 16 + 4 * (lane >> 4) + j;
+      if (row >= rows) continue;
+      uint16_t* drow = dst + (size_t)(row0 + row) * Ndim;
+      if (GATEUP) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const float gv = round_bf16(acc[mi][g][j]);
+          const float uv = round_bf16(acc[mi][g + 2][j]);
+          drow[nt * 128 + wv * 32 + g * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(gv) * uv);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          drow[nt * 256 + wv * 64 + g * 16 + (lane & 15)] = f32_to_bf16_bits(acc[mi][g][j]);
+      }
+    }
+  }
+}
+
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void k_gemm(int D, int I, int E, const uint16_t* __restrict__ src,
+                                               const int32_t* __restrict__ offsets,
+                                               const int32_t* __restrict__ sorted_token,
+                                               const int8_t* __restrict__ wp, const float* __restrict__ sp,
+                                               uint16_t* __restrict__ dst) {
+  __shared__ alignas(16) uint16_t a0[kGStageA];
+  __shared__ alignas(16) uint16_t a1[kGStageA];
+  __shared__ alignas(16) uint16_t a2[kGStageA];
+  __shared__ alignas(16) int8_t b0[kGStageB];
+  __shared__ alignas(16) int8_t b1[kGStageB];
+  __shared__ alignas(16) int8_t b2[kGStageB];
+  __shared__ int mtp[kMaxExperts + 1];
+  __shared__ int tok[kGM];
+  const int tid = threadIdx.x;
+  const int NT = GATEUP ? I / 128 : D / 256;
+  tile_prefix<kGM>(offsets, E, mtp);
+  const int ntiles = mtp[E] * NT;
+  const int per = (ntiles + 7) >> 3;
+  const int q = blockIdx.x >> 3;
+  if (q >= per) return;
+  const int L = (blockIdx.x & 7) * per + q;
+  if (L >= ntiles) return;
+  // L -> (expert, column tile, row chunk), row chunk fastest
+  const int e = tile_expert(mtp, E, L / NT);
+  const int nmt = mtp[e + 1] - mtp[e];
+  const int rem = L - mtp[e] * NT;
+  const int nt = rem / nmt;
+  const int mt = rem - nt * nmt;
+  const int row0 = offsets[e] + mt * kGM;
+  const int rows = min(kGM, offsets[e + 1] - row0);
+  tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
+  __syncthreads();
+  switch ((rows + 63) >> 6) {
+    case 1:
+      gemm_tile<GATEUP, 4>(tok, a0, a1, a2, b0, b1, b2, D, I, e, nt, row0, rows, src, wp, sp, dst);
+      break;
+    case 2:
+      gemm_tile<GATEUP, 8>(tok, a0, a1, a2, b0, b1, b2, D, I, e, nt, row0, rows, src, wp, sp, dst);
+      break;
+    case 3:
+      gemm_tile<GATEUP, 12>(tok, a0, a1, a2, b0, b1, b2, D, I, e, nt, row0, rows, src, wp, sp, dst);
+      break;
+    default:
+      gemm_tile<GATEUP, 16>(tok, a0, a1, a2, b0, b1, b2, D, I, e, nt, row0, rows, src, wp, sp, dst);
+      break;
   }
 }
 
@@ -673,6 +888,22 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
       else
         hipLaunchKernelGGL((k_down_decode<4, 2, 4, true>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
                            s2, yb);
+      return hipGetLastError();
+    }
+    return hipSuccess;
+  }
+  if (I % 128 == 0 && D % 256 == 0) {
+    const int upper_mt = (M + kGM - 1) / kGM + slots;
+    auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };
+    if (stages & kStageGateUp) {
+      hipLaunchKernelGGL((k_gemm<true>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb, offsets,
+                         sorted_token, w13, s13, hb);
+      hipError_t err = hipGetLastError();
+      if (err != hipSuccess) return err;
+    }
+    if (stages & kStageDown) {
+      hipLaunchKernelGGL((k_gemm<false>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb, offsets,
+                         sorted_token, w2, s2, yb);
       return hipGetLastError();
     }
     return hipSuccess;
