@@ -19,18 +19,24 @@ namespace kmoe {
 // ---------------------------------------------------------------------------
 // helpers
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+}
+
+// 16 int8 -> bf16(q * s) (s already rounded to bf16), one packed pair at a time
 __device__ __forceinline__ void dequant16(const uint4 q, const float s, bf16x8& lo, bf16x8& hi) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  uint32_t o[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int8_t b = (int8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
-    lo[j] = (__bf16)((float)b * s);
+    const uint32_t v = w[j >> 1];
+    const int sh = 16 * (j & 1);
+    const float a = (float)(int8_t)((v >> sh) & 0xffu);
+    const float b = (float)(int8_t)((v >> (sh + 8)) & 0xffu);
+    o[j] = pack_bf16x2(a * s, b * s);
   }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int8_t b = (int8_t)((w[2 + (j >> 2)] >> (8 * (j & 3))) & 0xffu);
-    hi[j] = (__bf16)((float)b * s);
-  }
+  lo = __builtin_bit_cast(bf16x8, uint4{o[0], o[1], o[2], o[3]});
+  hi = __builtin_bit_cast(bf16x8, uint4{o[4], o[5], o[6], o[7]});
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -476,35 +482,36 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
 }
 
 // ---------------------------------------------------------------------------
-// Prefill grouped GEMM: up to 256 rows x 256 columns per tile (gate/up: 128
+// Prefill grouped GEMM: up to 128 rows x 256 columns per tile (gate/up: 128
 // gate + 128 up columns, i.e. 128 columns of h; down: 256 output columns),
-// 64-deep k chunks, four waves.
+// 64-deep k chunks, four waves, two blocks per CU.
 //
-// A work item is (expert, chunk of up to 256 of its rows, column tile). Wave w
+// A work item is (expert, chunk of up to 128 of its rows, column tile). Wave w
 // owns all rows x 64 columns (four 16-column groups; for gate/up two gate
 // groups and the matching two up groups, so the SwiGLU epilogue pairs
 // registers of one lane) in accumulator tiles of v_mfma_f32_16x16x32_bf16.
 //
-// Global data reaches LDS by direct loads (global_load_lds_dwordx4), three
-// chunks deep, so no registers are spent on prefetch: A (activation rows,
-// gathered by token for gate/up) as [row][8 x 16 B] with the 16-byte pieces
-// XOR-swizzled by row, and each wave's raw int8 B (its 1 KB cell chunks, in
-// the packed layout a lane's 16 bytes are one column's 16 k = one MFMA B
-// fragment). Each chunk: issue chunk c+2's loads, read the wave's raw B and
-// dequantise it to bf16(q * bf16(s)), run the MFMAs with A fragments read one
-// tile ahead, wait for chunk c+1's loads, barrier. The barrier is the bare
-// s_barrier with explicit counter waits: a workgroup fence would also wait
-// for the chunk c+2 loads.
+// A (activation rows, gathered by token for gate/up) reaches LDS by direct
+// loads (global_load_lds_dwordx4) three chunks deep, stored [row][8 x 16 B]
+// with the 16-byte pieces XOR-swizzled by row. B never touches LDS: in the
+// packed layout a lane's 16 bytes of a cell chunk are one column's 16 k, i.e.
+// exactly its MFMA B fragment, so each wave loads its own four cells into
+// registers two chunks ahead and dequantises them to bf16(q * bf16(s)). Each
+// chunk: issue chunk c+2's loads (A first), dequantise B(c), run the MFMAs
+// with A fragments read one tile ahead, wait for chunk c+1's A, barrier. The
+// barrier is the bare s_barrier with explicit counter waits: a workgroup fence
+// would also wait for the chunk c+2 loads. Two blocks share a CU (about 53 KB
+// of LDS and at most 256 registers per lane each), so one block's barriers,
+// prologue and epilogue overlap the other's MFMAs.
 //
 // Rows past the expert's end are computed on a clamped copy of row 0 and
-// never stored; the tile body is instantiated for 4, 8, 12 or 16 row tiles.
-// Work items are ordered (expert, column tile, row chunk) and consecutive
-// items go to the same XCD, so the row chunks of one expert reuse its
-// weights in that XCD's L2.
+// never stored; the tile body is instantiated for 4 or 8 row tiles. Work
+// items are ordered (expert, column tile, row chunk) and consecutive items go
+// to the same XCD, so the row chunks of one expert reuse its weights in that
+// XCD's L2.
 // ---------------------------------------------------------------------------
-constexpr int kGM = 256;  // rows per tile
-constexpr int kGStageA = kGM * 64;   // bf16 per A stage
-constexpr int kGStageB = 4 * 4 * 1024;  // bytes per B stage: 4 waves x 4 cells x 1 KB
+constexpr int kGM = 128;            // rows per tile
+constexpr int kGStageA = kGM * 64;  // bf16 per A stage
 
 typedef __attribute__((address_space(1))) void gmem_void;
 typedef __attribute__((address_space(3))) void lds_void;
@@ -526,14 +533,14 @@ __device__ __forceinline__ void wait_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// 16-byte piece p of row r of an A stage
+// element offset of 16-byte piece p of row r in an A stage
 __device__ __forceinline__ int a_swz(int r, int p) { return r * 64 + ((p ^ (r & 7)) << 3); }
 
 template <bool GATEUP, int MT>
-__device__ __forceinline__ void gemm_tile(const int* tok, uint16_t* A0, uint16_t* A1, uint16_t* A2, int8_t* B0,
-                                          int8_t* B1, int8_t* B2, int D, int I, int e, int nt, int row0, int rows,
-                                          const uint16_t* __restrict__ src, const int8_t* __restrict__ wp,
-                                          const float* __restrict__ sp, uint16_t* __restrict__ dst) {
+__device__ __forceinline__ void gemm_tile(const int* tok, uint16_t* A0, uint16_t* A1, uint16_t* A2, int D, int I,
+                                          int e, int nt, int row0, int rows, const uint16_t* __restrict__ src,
+                                          const int8_t* __restrict__ wp, const float* __restrict__ sp,
+                                          uint16_t* __restrict__ dst) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int Kdim = GATEUP ? D : I;
   const int Ndim = GATEUP ? I : D;
@@ -570,23 +577,23 @@ __device__ __forceinline__ void gemm_tile(const int* tok, uint16_t* A0, uint16_t
 #pragma unroll
     for (int g = 0; g < 4; ++g) acc[mi][g] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  constexpr int kLoads = AJ + 4;  // direct loads per lane per chunk
-#define KMOE_DMA(c, AS, BS)                                                              \
-  {                                                                                      \
-    const int cc = (c);                                                                  \
-    _Pragma("unroll") for (int j = 0; j < AJ; ++j)                                       \
-        dma16(src + aoff[j] + cc * 64, AS + (wv * AJ + j) * 512);                        \
-    _Pragma("unroll") for (int g = 0; g < 4; ++g)                                        \
-        dma16(bp[g] + (size_t)cc * 1024, BS + (wv * 4 + g) * 1024);                      \
+  uint4 rb0[4], rb1[4], rb2[4];  // raw B of three consecutive chunks, rotated statically
+  // per chunk: AJ direct A loads, then 4 B loads; the barrier of chunk c waits
+  // for A(c+1), followed by B(c+1), A(c+2), B(c+2)
+  constexpr int kAfter = 4 + AJ + 4;
+#define KMOE_LOAD(c, AS, RB)                                                        \
+  {                                                                                 \
+    const int cc = (c);                                                             \
+    _Pragma("unroll") for (int j = 0; j < AJ; ++j)                                  \
+        dma16(src + aoff[j] + cc * 64, AS + (wv * AJ + j) * 512);                   \
+    _Pragma("unroll") for (int g = 0; g < 4; ++g)                                   \
+        RB[g] = *reinterpret_cast<const uint4*>(bp[g] + (size_t)cc * 1024);         \
   }
-#define KMOE_STEP(c, AS, BS, AN, BN)                                                                      \
+#define KMOE_STEP(c, AS, AN, RB, RN)                                                                      \
   {                                                                                                       \
-    KMOE_DMA(min((c) + 2, KC - 1), AN, BN)                                                                \
+    KMOE_LOAD(min((c) + 2, KC - 1), AN, RN)                                                               \
     bf16x8 lo[4], hi[4];                                                                                  \
-    _Pragma("unroll") for (int g = 0; g < 4; ++g) {                                                       \
-      const uint4 q = *reinterpret_cast<const uint4*>(BS + (wv * 4 + g) * 1024 + lane * 16);             \
-      dequant16(q, sc[g], lo[g], hi[g]);                                                                  \
-    }                                                                                                     \
+    _Pragma("unroll") for (int g = 0; g < 4; ++g) dequant16(RB[g], sc[g], lo[g], hi[g]);                  \
     _Pragma("unroll") for (int st = 0; st < 2; ++st) {                                                    \
       const int p = 2 * (lane >> 4) + st;                                                                 \
       _Pragma("unroll") for (int mi = 0; mi < MT; ++mi) {                                                 \
@@ -594,25 +601,25 @@ __device__ __forceinline__ void gemm_tile(const int* tok, uint16_t* A0, uint16_t
         _Pragma("unroll") for (int g = 0; g < 4; ++g) acc[mi][g] = mfma16(a, st ? hi[g] : lo[g], acc[mi][g]); \
       }                                                                                                   \
     }                                                                                                     \
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);                                                    \
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                                                    \
     _Pragma("unroll") for (int i = 0; i < 2 * MT; ++i) {                                                  \
       __builtin_amdgcn_sched_group_barrier(0x002, 160 / (2 * MT) + 1, 0);                                 \
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                                  \
       if (i + 2 < 2 * MT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                              \
     }                                                                                                     \
-    wait_barrier<kLoads>();                                                                               \
+    wait_barrier<kAfter>();                                                                               \
   }
 
-  KMOE_DMA(0, A0, B0)
-  KMOE_DMA(min(1, KC - 1), A1, B1)
-  wait_barrier<kLoads>();
+  KMOE_LOAD(0, A0, rb0)
+  KMOE_LOAD(min(1, KC - 1), A1, rb1)
+  wait_barrier<kAfter>();
   for (int c = 0; c < KC; c += 3) {
-    KMOE_STEP(c, A0, B0, A2, B2)
-    if (c + 1 < KC) KMOE_STEP(c + 1, A1, B1, A0, B0)
-    if (c + 2 < KC) KMOE_STEP(c + 2, A2, B2, A1, B1)
+    KMOE_STEP(c, A0, A2, rb0, rb2)
+    if (c + 1 < KC) KMOE_STEP(c + 1, A1, A0, rb1, rb0)
+    if (c + 2 < KC) KMOE_STEP(c + 2, A2, A1, rb2, rb1)
   }
 #undef KMOE_STEP
-#undef KMOE_DMA
+#undef KMOE_LOAD
 
   // epilogue: lane holds rows 4*(lane/16)+j of each 16x16 tile, column lane%16;
   // one tile row at a time (the scheduling barrier keeps the accumulator reads
@@ -642,17 +649,14 @@ __device__ __forceinline__ void gemm_tile(const int* tok, uint16_t* A0, uint16_t
 }
 
 template <bool GATEUP>
-__global__ __launch_bounds__(256) void k_gemm(int D, int I, int E, const uint16_t* __restrict__ src,
-                                               const int32_t* __restrict__ offsets,
-                                               const int32_t* __restrict__ sorted_token,
-                                               const int8_t* __restrict__ wp, const float* __restrict__ sp,
-                                               uint16_t* __restrict__ dst) {
+__global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint16_t* __restrict__ src,
+                                                  const int32_t* __restrict__ offsets,
+                                                  const int32_t* __restrict__ sorted_token,
+                                                  const int8_t* __restrict__ wp, const float* __restrict__ sp,
+                                                  uint16_t* __restrict__ dst) {
   __shared__ alignas(16) uint16_t a0[kGStageA];
   __shared__ alignas(16) uint16_t a1[kGStageA];
   __shared__ alignas(16) uint16_t a2[kGStageA];
-  __shared__ alignas(16) int8_t b0[kGStageB];
-  __shared__ alignas(16) int8_t b1[kGStageB];
-  __shared__ alignas(16) int8_t b2[kGStageB];
   __shared__ int mtp[kMaxExperts + 1];
   __shared__ int tok[kGM];
   const int tid = threadIdx.x;
@@ -672,22 +676,12 @@ __global__ __launch_bounds__(256) void k_gemm(int D, int I, int E, const uint16_
   const int mt = rem - nt * nmt;
   const int row0 = offsets[e] + mt * kGM;
   const int rows = min(kGM, offsets[e + 1] - row0);
-  tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
+  if (tid < kGM) tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
   __syncthreads();
-  switch ((rows + 63) >> 6) {
-    case 1:
-      gemm_tile<GATEUP, 4>(tok, a0, a1, a2, b0, b1, b2, D, I, e, nt, row0, rows, src, wp, sp, dst);
-      break;
-    case 2:
-      gemm_tile<GATEUP, 8>(tok, a0, a1, a2, b0, b1, b2, D, I, e, nt, row0, rows, src, wp, sp, dst);
-      break;
-    case 3:
-      gemm_tile<GATEUP, 12>(tok, a0, a1, a2, b0, b1, b2, D, I, e, nt, row0, rows, src, wp, sp, dst);
-      break;
-    default:
-      gemm_tile<GATEUP, 16>(tok, a0, a1, a2, b0, b1, b2, D, I, e, nt, row0, rows, src, wp, sp, dst);
-      break;
-  }
+  if (rows <= 64)
+    gemm_tile<GATEUP, 4>(tok, a0, a1, a2, D, I, e, nt, row0, rows, src, wp, sp, dst);
+  else
+    gemm_tile<GATEUP, 8>(tok, a0, a1, a2, D, I, e, nt, row0, rows, src, wp, sp, dst);
 }
 
 // ---------------------------------------------------------------------------
