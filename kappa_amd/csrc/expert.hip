@@ -19,8 +19,11 @@ namespace kmoe {
 // ---------------------------------------------------------------------------
 // helpers
 // ---------------------------------------------------------------------------
+// two floats -> one dword of bf16 (RNE), a in the low half: one v_cvt_pk_bf16_f32
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
 
 // 16 int8 -> bf16(q * s) (s already rounded to bf16), one packed pair at a time
@@ -46,38 +49,42 @@ __device__ __forceinline__ floatx4 mfma16(const bf16x8 a, const bf16x8 b, const 
 }
 
 // Block-wide tile prefix over experts: mtp[e] = sum_{e' < e} ceil(group_size[e'] / BM), mtp[E] = total.
-// blockDim.x must be 256.
+// The first 256 threads compute it (E <= 1024); blockDim.x must be a multiple of 64, at least 256.
+// wsum: 4 ints of LDS scratch.
 template <int BM>
-__device__ void tile_prefix(const int32_t* __restrict__ offsets, int E, int* mtp) {
-  __shared__ int wsum[4];
+__device__ void tile_prefix(const int32_t* __restrict__ offsets, int E, int* mtp, int* wsum) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   int c[4];
-  int local = 0;
+  int local = 0, incl = 0;
+  if (tid < 256) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid * 4 + i;
-    c[i] = 0;
-    if (e < E) c[i] = (offsets[e + 1] - offsets[e] + BM - 1) / BM;
-    local += c[i];
-  }
-  int incl = local;
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid * 4 + i;
+      c[i] = 0;
+      if (e < E) c[i] = (offsets[e + 1] - offsets[e] + BM - 1) / BM;
+      local += c[i];
+    }
+    incl = local;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int v = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += v;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
+    }
+    if (lane == 63) wsum[wv] = incl;
   }
-  if (lane == 63) wsum[wv] = incl;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wv; ++w) base += wsum[w];
-  int run = base + incl - local;
+  if (tid < 256) {
+    int base = 0;
+    for (int w = 0; w < wv; ++w) base += wsum[w];
+    int run = base + incl - local;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid * 4 + i;
-    if (e < E) mtp[e] = run;
-    run += c[i];
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid * 4 + i;
+      if (e < E) mtp[e] = run;
+      run += c[i];
+    }
+    if (tid == 255) mtp[E] = base + incl;
   }
-  if (tid == 255) mtp[E] = base + incl;
   __syncthreads();
 }
 
@@ -335,11 +342,12 @@ struct PrefillLds {
   alignas(16) uint16_t b[2][2][8][64][8];  // [buf][sub-step][col group][lane][8 bf16]
   int mtp[kMaxExperts + 1];
   int tok[kBM];
+  int wsum[4];
 };
 
 __device__ __forceinline__ bool prefill_tile(const int32_t* __restrict__ offsets, int E, int NT, PrefillLds& s,
                                              int& e, int& row0, int& rows, int& nt) {
-  tile_prefix<kBM>(offsets, E, s.mtp);
+  tile_prefix<kBM>(offsets, E, s.mtp, s.wsum);
   const int ntiles = s.mtp[E] * NT;
   const int per = (ntiles + 7) >> 3;
   const int q = blockIdx.x >> 3;
@@ -482,151 +490,160 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
 }
 
 // ---------------------------------------------------------------------------
-// Prefill grouped GEMM: up to 128 rows x 256 columns per tile (gate/up: 128
-// gate + 128 up columns, i.e. 128 columns of h; down: 256 output columns),
-// 64-deep k chunks, four waves, two blocks per CU.
+// Prefill grouped GEMM over (expert, row tile, column tile) work items.
 //
-// A work item is (expert, chunk of up to 128 of its rows, column tile). Wave w
-// owns all rows x 64 columns (four 16-column groups; for gate/up two gate
-// groups and the matching two up groups, so the SwiGLU epilogue pairs
-// registers of one lane) in accumulator tiles of v_mfma_f32_16x16x32_bf16.
+// A block of four waves computes up to 128 rows x 256 B columns (gate/up: 128
+// gate + 128 up columns, i.e. 128 columns of h; down: 256 output columns);
+// two blocks share a CU. Wave w owns the 16-column cells 4w .. 4w+3 (gate/up:
+// two gate cells and the matching two up cells, so the SwiGLU epilogue pairs
+// registers of one lane) for all rows, in accumulator tiles of
+// v_mfma_f32_16x16x32_bf16, and dequantises its cells to bf16(q * bf16(s)) in
+// registers once per 64-deep k chunk.
 //
-// A (activation rows, gathered by token for gate/up) reaches LDS by direct
-// loads (global_load_lds_dwordx4) three chunks deep, stored [row][8 x 16 B]
-// with the 16-byte pieces XOR-swizzled by row. B never touches LDS: in the
-// packed layout a lane's 16 bytes of a cell chunk are one column's 16 k, i.e.
-// exactly its MFMA B fragment, so each wave loads its own four cells into
-// registers two chunks ahead and dequantises them to bf16(q * bf16(s)). Each
-// chunk: issue chunk c+2's loads (A first), dequantise B(c), run the MFMAs
-// with A fragments read one tile ahead, wait for chunk c+1's A, barrier. The
-// barrier is the bare s_barrier with explicit counter waits: a workgroup fence
-// would also wait for the chunk c+2 loads. Two blocks share a CU (about 53 KB
-// of LDS and at most 256 registers per lane each), so one block's barriers,
-// prologue and epilogue overlap the other's MFMAs.
+// Both operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4):
+// A (activation rows, gathered by token for gate/up) in a 2-stage ring as
+// [row][8 x 16 B] with the 16-byte pieces XOR-swizzled by row, B (the packed
+// cells, whose 16 bytes per lane are exactly one lane's MFMA fragment of one
+// column) in a 3-stage ring, so the weights, which come from HBM, are
+// requested two chunks ahead and the activation rows, mostly L2 hits, one
+// chunk ahead. 80 KB per block: two blocks fill the CU's LDS. The loads are
+// inline asm, so the compiler's wait-count pass does not see them: every wave
+// issues the same loads in the same order and the chunk loop waits for them
+// itself (vmcnt is in-order), then a barrier publishes the stage and frees
+// the ones read last.
 //
-// Rows past the expert's end are computed on a clamped copy of row 0 and
-// never stored; the tile body is instantiated for 4 or 8 row tiles. Work
-// items are ordered (expert, column tile, row chunk) and consecutive items go
-// to the same XCD, so the row chunks of one expert reuse its weights in that
-// XCD's L2.
+// Rows past the expert's end are loaded from a clamped copy of row 0 and never
+// stored; the loop body is instantiated for 8, 4, 2 and 1 active 16-row
+// tiles. Work items are ordered (expert, column tile, row tile) and
+// consecutive items go to the same XCD, so the row tiles of one expert share
+// its weights, and the column tiles its rows, in that XCD's L2.
 // ---------------------------------------------------------------------------
-constexpr int kGM = 128;            // rows per tile
-constexpr int kGStageA = kGM * 64;  // bf16 per A stage
-
-typedef __attribute__((address_space(1))) void gmem_void;
 typedef __attribute__((address_space(3))) void lds_void;
 
-// 16 bytes per lane from global memory straight into LDS: lane l's data lands
-// at lds_base + 16 * l (lds_base is wave-uniform).
-__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((gmem_void*)g, (lds_void*)lds_base, 16, 0, 0);
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
+
+// 16 bytes per lane from global memory (sbase + voff) into LDS at lds + 16 * lane.
+// sbase and lds must be wave-uniform.
+__device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
 }
 
-// s_waitcnt vmcnt(n) lgkmcnt(0) (gfx9 encoding), then a workgroup barrier.
-// The compiler-only fences keep LDS accesses on their side of the barrier.
+// Wait until at most N of this wave's vector-memory loads are outstanding and
+// its LDS reads are done, then a workgroup barrier. The "memory" clobber keeps
+// every LDS access on its side.
 template <int N>
-__device__ __forceinline__ void wait_barrier() {
-  static_assert(N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+__device__ __forceinline__ void vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// element offset of 16-byte piece p of row r in an A stage
-__device__ __forceinline__ int a_swz(int r, int p) { return r * 64 + ((p ^ (r & 7)) << 3); }
+// silu(g) * u for the MFMA epilogue: hardware exp2 and reciprocal (a few fp32
+// ulps from g / (1 + expf(-g)); the product is rounded to bf16 next).
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
+// Element offset of 16-byte piece p of row r in an A stage: [row][8 x 16 B],
+// pieces XOR-swizzled by (r >> 1) & 7. A row is half the 256-byte bank width,
+// so this puts the 16 rows one fragment read touches on 16 distinct 16-byte
+// bank groups.
+__device__ __forceinline__ int a_piece(int r, int p) { return p ^ (r & 7); }
+__device__ __forceinline__ int a_swz(int r, int p) { return r * 64 + (a_piece(r, p) << 3); }
+
+// 8 int8 (two dwords) -> bf16(q * s), s already rounded to bf16
+__device__ __forceinline__ bf16x8 dequant8(const uint32_t w0, const uint32_t w1, const float s) {
+  const uint32_t w[2] = {w0, w1};
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t v = w[j >> 1];
+    const int sh = 16 * (j & 1);
+    o[j] = pack_bf16x2((float)(int8_t)((v >> sh) & 0xffu) * s, (float)(int8_t)((v >> (sh + 8)) & 0xffu) * s);
+  }
+  return __builtin_bit_cast(bf16x8, uint4{o[0], o[1], o[2], o[3]});
+}
+
+constexpr int kGemmRows = 128;                // rows per tile
+constexpr int kGemmA = kGemmRows * 128;       // A stage: 128 rows x 64 bf16 (16 KB)
+constexpr int kGemmB = 16 * 1024;             // B stage: 16 cells x 64 k x 16 columns int8
+constexpr int kGemmNA = 2, kGemmNB = 3;       // ring depths
+constexpr int kGemmLds = kGemmNA * kGemmA + kGemmNB * kGemmB;  // 80 KB: two blocks fill the CU's LDS
+constexpr int kGemmAJ = 4, kGemmBJ = 4;       // loads per wave per chunk (A: 8 rows each, B: one cell)
+
+// Per-wave load descriptors of one tile.
+struct GemmLoads {
+  uint32_t avoff[kGemmAJ];  // byte offsets (per lane) of this wave's A loads in src
+  const int8_t* bsrc[4];    // this wave's four B cells, at chunk 0
+  float sc[4];              // their scales (column lane % 16)
+};
 
 template <bool GATEUP, int MT>
-__device__ __forceinline__ void gemm_tile(const int* tok, uint16_t* A0, uint16_t* A1, uint16_t* A2, int D, int I,
-                                          int e, int nt, int row0, int rows, const uint16_t* __restrict__ src,
-                                          const int8_t* __restrict__ wp, const float* __restrict__ sp,
-                                          uint16_t* __restrict__ dst) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int Kdim = GATEUP ? D : I;
-  const int Ndim = GATEUP ? I : D;
-  constexpr int AJ = MT / 2;  // A load instructions per wave per chunk (8 rows each)
-  // A: instruction j of wave w covers rows 8q .. 8q+7, q = w*AJ + j; lane -> (row, piece)
-  uint32_t aoff[AJ];  // element offsets into src (src holds < 2^32 elements)
-#pragma unroll
-  for (int j = 0; j < AJ; ++j) {
-    const int r = 8 * (wv * AJ + j) + (lane >> 3);
-    const int t = tok[r] >= 0 ? tok[r] : tok[0];
-    aoff[j] = (uint32_t)t * (uint32_t)Kdim + (((lane & 7) ^ (r & 7)) << 3);
-  }
-  // B: this wave's four 16-column cells
-  const int8_t* bp[4];
-  float sc[4];
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    if (GATEUP) {
-      const int which = g >> 1;                   // 0: gate, 1: up
-      const int igl = nt * 8 + wv * 2 + (g & 1);  // 16-column group of h
-      const size_t cid = ((size_t)e * (I >> 4) + igl) * 2 + which;
-      bp[g] = wp + cid * (size_t)(D >> 4) * 256 + lane * 16;
-      sc[g] = sp[cid * 16 + (lane & 15)];
-    } else {
-      const int dg = nt * 16 + wv * 4 + g;
-      bp[g] = wp + ((size_t)e * (D >> 4) + dg) * (size_t)(I >> 4) * 256 + lane * 16;
-      sc[g] = sp[(size_t)e * D + dg * 16 + (lane & 15)];
-    }
-  }
-  const int KC = Kdim >> 6;
+__device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, int KC, int wv, int rows, int row0,
+                                          int nt, const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                          int Ndim) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t lds0 = lds_addr(smem);
+  const uint8_t* const bring = smem + kGemmNA * kGemmA;
   floatx4 acc[MT][4];
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
     for (int g = 0; g < 4; ++g) acc[mi][g] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  uint4 rb0[4], rb1[4], rb2[4];  // raw B of three consecutive chunks, rotated statically
-  // per chunk: AJ direct A loads, then 4 B loads; the barrier of chunk c waits
-  // for A(c+1), followed by B(c+1), A(c+2), B(c+2)
-  constexpr int kAfter = 4 + AJ + 4;
-#define KMOE_LOAD(c, AS, RB)                                                        \
-  {                                                                                 \
-    const int cc = (c);                                                             \
-    _Pragma("unroll") for (int j = 0; j < AJ; ++j)                                  \
-        dma16(src + aoff[j] + cc * 64, AS + (wv * AJ + j) * 512);                   \
-    _Pragma("unroll") for (int g = 0; g < 4; ++g)                                   \
-        RB[g] = *reinterpret_cast<const uint4*>(bp[g] + (size_t)cc * 1024);         \
+  auto issue_a = [&](int c) {
+    const uint32_t st = lds0 + (uint32_t)((c & 1) * kGemmA + wv * kGemmAJ * 1024);
+    const uint16_t* abase = src + c * 64;
+#pragma unroll
+    for (int j = 0; j < kGemmAJ; ++j) dma16(gl.avoff[j], abase, st + j * 1024);
+  };
+  auto issue_b = [&](int c) {
+    const uint32_t st = lds0 + (uint32_t)(kGemmNA * kGemmA + (c % kGemmNB) * kGemmB + wv * 4096);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) dma16(lane * 16, gl.bsrc[g] + c * 1024, st + g * 1024);
+  };
+
+  // Issue order: B(0), A(0), B(1); then iteration c issues A(c+1), B(c+2) and
+  // at its end waits for A(c+1) and B(c+1) (only B(c+2) may be outstanding).
+  issue_b(0);
+  issue_a(0);
+  if (1 < KC) {
+    issue_b(1);
+    vm_barrier<kGemmBJ>();
+  } else {
+    vm_barrier<0>();
   }
-#define KMOE_STEP(c, AS, AN, RB, RN)                                                                      \
-  {                                                                                                       \
-    KMOE_LOAD(min((c) + 2, KC - 1), AN, RN)                                                               \
-    bf16x8 lo[4], hi[4];                                                                                  \
-    _Pragma("unroll") for (int g = 0; g < 4; ++g) dequant16(RB[g], sc[g], lo[g], hi[g]);                  \
-    _Pragma("unroll") for (int st = 0; st < 2; ++st) {                                                    \
-      const int p = 2 * (lane >> 4) + st;                                                                 \
-      _Pragma("unroll") for (int mi = 0; mi < MT; ++mi) {                                                 \
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(AS + a_swz(mi * 16 + (lane & 15), p));         \
-        _Pragma("unroll") for (int g = 0; g < 4; ++g) acc[mi][g] = mfma16(a, st ? hi[g] : lo[g], acc[mi][g]); \
-      }                                                                                                   \
-    }                                                                                                     \
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                                                    \
-    _Pragma("unroll") for (int i = 0; i < 2 * MT; ++i) {                                                  \
-      __builtin_amdgcn_sched_group_barrier(0x002, 160 / (2 * MT) + 1, 0);                                 \
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                                                  \
-      if (i + 2 < 2 * MT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                              \
-    }                                                                                                     \
-    wait_barrier<kAfter>();                                                                               \
+  for (int c = 0; c < KC; ++c) {
+    if (c + 1 < KC) issue_a(c + 1);
+    if (c + 2 < KC) issue_b(c + 2);
+    uint4 raw[4];
+    const uint8_t* bp = bring + (c % kGemmNB) * kGemmB + wv * 4096 + lane * 16;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) raw[g] = *reinterpret_cast<const uint4*>(bp + g * 1024);
+    bf16x8 lo[4], hi[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) dequant16(raw[g], gl.sc[g], lo[g], hi[g]);
+    const uint16_t* As = reinterpret_cast<const uint16_t*>(smem + (c & 1) * kGemmA);
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int p = 2 * (lane >> 4) + st;
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(As + a_swz(mi * 16 + (lane & 15), p));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) acc[mi][g] = mfma16(a, st ? hi[g] : lo[g], acc[mi][g]);
+      }
+    }
+    if (c + 1 < KC) {
+      if (c + 2 < KC)
+        vm_barrier<kGemmBJ>();
+      else
+        vm_barrier<0>();
+    }
   }
 
-  KMOE_LOAD(0, A0, rb0)
-  KMOE_LOAD(min(1, KC - 1), A1, rb1)
-  wait_barrier<kAfter>();
-  for (int c = 0; c < KC; c += 3) {
-    KMOE_STEP(c, A0, A2, rb0, rb2)
-    if (c + 1 < KC) KMOE_STEP(c + 1, A1, A0, rb1, rb0)
-    if (c + 2 < KC) KMOE_STEP(c + 2, A2, A1, rb2, rb1)
-  }
-#undef KMOE_STEP
-#undef KMOE_LOAD
-
-  // epilogue: lane holds rows 4*(lane/16)+j of each 16x16 tile, column lane%16;
-  // one tile row at a time (the scheduling barrier keeps the accumulator reads
-  // from being hoisted all at once)
+  // epilogue: lane holds rows 4*(lane/16)+j of each 16x16 tile, column lane%16
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi) {
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = mi * 16 + 4 * (lane >> 4) + j;
@@ -637,51 +654,89 @@ __device__ __forceinline__ void gemm_tile(const int* tok, uint16_t* A0, uint16_t
         for (int g = 0; g < 2; ++g) {
           const float gv = round_bf16(acc[mi][g][j]);
           const float uv = round_bf16(acc[mi][g + 2][j]);
-          drow[nt * 128 + wv * 32 + g * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(gv) * uv);
+          drow[nt * 128 + wv * 32 + g * 16 + (lane & 15)] = f32_to_bf16_bits(silu_mul_fast(gv, uv));
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          drow[nt * 256 + wv * 64 + g * 16 + (lane & 15)] = f32_to_bf16_bits(acc[mi][g][j]);
+        for (int g = 0; g < 4; ++g) drow[nt * 256 + wv * 64 + g * 16 + (lane & 15)] = f32_to_bf16_bits(acc[mi][g][j]);
       }
     }
   }
 }
 
+// GATEUP = true: A rows gathered from x by token, B = gate|up cells, epilogue
+// SwiGLU -> h_sorted. GATEUP = false: A = h_sorted rows, B = down, epilogue ->
+// y_sorted. src must span fewer than 2^32 bytes (32-bit load offsets).
 template <bool GATEUP>
 __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint16_t* __restrict__ src,
                                                   const int32_t* __restrict__ offsets,
                                                   const int32_t* __restrict__ sorted_token,
                                                   const int8_t* __restrict__ wp, const float* __restrict__ sp,
                                                   uint16_t* __restrict__ dst) {
-  __shared__ alignas(16) uint16_t a0[kGStageA];
-  __shared__ alignas(16) uint16_t a1[kGStageA];
-  __shared__ alignas(16) uint16_t a2[kGStageA];
-  __shared__ int mtp[kMaxExperts + 1];
-  __shared__ int tok[kGM];
-  const int tid = threadIdx.x;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kGemmLds];
+  // set-up scratch inside the ring (no loads are in flight yet)
+  int* const mtp = reinterpret_cast<int*>(smem);
+  int* const tok = mtp + kMaxExperts + 1;
+  int* const wsum = tok + kGemmRows;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int NT = GATEUP ? I / 128 : D / 256;
-  tile_prefix<kGM>(offsets, E, mtp);
+  tile_prefix<kGemmRows>(offsets, E, mtp, wsum);
   const int ntiles = mtp[E] * NT;
   const int per = (ntiles + 7) >> 3;
   const int q = blockIdx.x >> 3;
   if (q >= per) return;
   const int L = (blockIdx.x & 7) * per + q;
   if (L >= ntiles) return;
-  // L -> (expert, column tile, row chunk), row chunk fastest
-  const int e = tile_expert(mtp, E, L / NT);
-  const int nmt = mtp[e + 1] - mtp[e];
+  // L -> (expert, column tile, row tile), row tile fastest
+  const int e = __builtin_amdgcn_readfirstlane(tile_expert(mtp, E, L / NT));
+  const int nmt_e = mtp[e + 1] - mtp[e];
   const int rem = L - mtp[e] * NT;
-  const int nt = rem / nmt;
-  const int mt = rem - nt * nmt;
-  const int row0 = offsets[e] + mt * kGM;
-  const int rows = min(kGM, offsets[e + 1] - row0);
-  if (tid < kGM) tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
+  const int nt = __builtin_amdgcn_readfirstlane(rem / nmt_e);
+  const int mt = rem - nt * nmt_e;
+  const int row0 = __builtin_amdgcn_readfirstlane(offsets[e] + mt * kGemmRows);
+  const int rows = __builtin_amdgcn_readfirstlane(min(kGemmRows, offsets[e + 1] - row0));
+  if (tid < kGemmRows) tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
   __syncthreads();
-  if (rows <= 64)
-    gemm_tile<GATEUP, 4>(tok, a0, a1, a2, D, I, e, nt, row0, rows, src, wp, sp, dst);
+
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int Kdim = GATEUP ? D : I;
+  const int Ndim = GATEUP ? I : D;
+  GemmLoads gl;
+  // A load j of wave wv covers tile rows 8q .. 8q+7, q = wv * 4 + j: lane -> (row, LDS piece lane % 8)
+#pragma unroll
+  for (int j = 0; j < kGemmAJ; ++j) {
+    const int r = 8 * (wv * kGemmAJ + j) + (lane >> 3);
+    const int t = tok[r] >= 0 ? tok[r] : tok[0];
+    gl.avoff[j] = ((uint32_t)t * (uint32_t)Kdim + (uint32_t)(a_piece(r, lane & 7) << 3)) * 2u;
+  }
+  // this wave's cells: gate/up -> (which = g >> 1, h group nt*8 + 2*wv + (g & 1)); down -> column group nt*16 + 4*wv + g
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    if (GATEUP) {
+      const size_t cid = ((size_t)e * (I >> 4) + nt * 8 + 2 * wv + (g & 1)) * 2 + (g >> 1);
+      gl.bsrc[g] = wp + cid * (size_t)(D >> 4) * 256;
+      gl.sc[g] = sp[cid * 16 + (lane & 15)];
+    } else {
+      const size_t dg = (size_t)e * (D >> 4) + nt * 16 + 4 * wv + g;
+      gl.bsrc[g] = wp + dg * (size_t)(I >> 4) * 256;
+      gl.sc[g] = sp[dg * 16 + (lane & 15)];
+    }
+  }
+  // consume the scale loads here, so the compiler's waits for them sit before
+  // the chunk loop (inside it they would also drain the ring's loads); and no
+  // wave may start loading into the ring while another still reads tok
+  asm volatile("" ::"v"(gl.sc[0]), "v"(gl.sc[1]), "v"(gl.sc[2]), "v"(gl.sc[3]));
+  __syncthreads();
+  const int KC = Kdim >> 6;
+  const int nmt = (rows + 15) >> 4;
+  if (nmt > 4)
+    gemm_tile<GATEUP, 8>(smem, gl, KC, wv, rows, row0, nt, src, dst, Ndim);
+  else if (nmt > 2)
+    gemm_tile<GATEUP, 4>(smem, gl, KC, wv, rows, row0, nt, src, dst, Ndim);
+  else if (nmt == 2)
+    gemm_tile<GATEUP, 2>(smem, gl, KC, wv, rows, row0, nt, src, dst, Ndim);
   else
-    gemm_tile<GATEUP, 8>(tok, a0, a1, a2, D, I, e, nt, row0, rows, src, wp, sp, dst);
+    gemm_tile<GATEUP, 1>(smem, gl, KC, wv, rows, row0, nt, src, dst, Ndim);
 }
 
 // ---------------------------------------------------------------------------
@@ -886,8 +941,10 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
     }
     return hipSuccess;
   }
-  if (I % 128 == 0 && D % 256 == 0) {
-    const int upper_mt = (M + kGM - 1) / kGM + slots;
+  // 32-bit load offsets: the gathered source must span fewer than 2^32 bytes
+  const bool small_src = (uint64_t)T * D * 2 < (1ull << 32) && (uint64_t)M * I * 2 < (1ull << 32);
+  if (I % 128 == 0 && D % 256 == 0 && small_src) {
+    const int upper_mt = (M + kGemmRows - 1) / kGemmRows + slots;
     auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };
     if (stages & kStageGateUp) {
       hipLaunchKernelGGL((k_gemm<true>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb, offsets,

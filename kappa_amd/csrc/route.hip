@@ -316,29 +316,69 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, i
   __shared__ unsigned long long mask[kMaxExperts];
   __shared__ int base[kMaxExperts];
   __shared__ int wsum[4], wact[4];
+  __shared__ int red_tot[4 * 256], red_bef[4 * 256];
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   chunk_masks(T, E, K, b, topk_idx, mask);
 
   // this thread's experts: 4*tid .. 4*tid+3
   int tot[4], bef[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    tot[i] = 0;
+    bef[i] = 0;
+  }
+  if (hist) {
+    // Chunk totals: the Q = ceil(E/4) expert quads are summed over the chunks
+    // by G = 256/Q thread groups (group g takes chunks g, g+G, ...), then the
+    // quad owner adds the groups' partials from LDS. Integer sums: any order.
+    const int Q = (E + 3) >> 2, G = 256 / Q;
+    const int q = tid % Q, gi = tid / Q;
+    int pt[4] = {0, 0, 0, 0}, pb[4] = {0, 0, 0, 0};
+    if (gi < G) {
+      const bool vec4 = (E & 3) == 0;
+#pragma unroll 4
+      for (int bb = gi; bb < nblk; bb += G) {
+        const int32_t* hp = hist + (int64_t)bb * E + 4 * q;
+        int h[4];
+        if (vec4) {
+          const int4 v = *reinterpret_cast<const int4*>(hp);
+          h[0] = v.x, h[1] = v.y, h[2] = v.z, h[3] = v.w;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) h[i] = 4 * q + i < E ? hp[i] : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pt[i] += h[i];
+          pb[i] += bb < b ? h[i] : 0;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red_tot[i * 256 + tid] = pt[i];
+      red_bef[i * 256 + tid] = pb[i];
+    }
+    __syncthreads();
+    if (tid < Q) {
+      for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          tot[i] += red_tot[i * 256 + g * Q + tid];
+          bef[i] += red_bef[i * 256 + g * Q + tid];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * tid + i < E) tot[i] = __popcll(mask[4 * tid + i]);
+  }
   int lsum = 0, lact = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int e = 4 * tid + i;
-    tot[i] = 0;
-    bef[i] = 0;
-    if (e < E) {
-      if (hist) {
-        for (int bb = 0; bb < nblk; ++bb) {
-          const int h = hist[(int64_t)bb * E + e];
-          tot[i] += h;
-          bef[i] += bb < b ? h : 0;
-        }
-      } else {
-        tot[i] = __popcll(mask[e]);
-      }
-    }
+    if (4 * tid + i >= E) tot[i] = bef[i] = 0;
     lsum += tot[i];
     lact += tot[i] > 0;
   }
