@@ -86,6 +86,104 @@ __device__ __forceinline__ float load_scale(const void* scale, int scale_bf16, i
 //   w_j = expf(l_j - l_0) / sum_{i<K} expf(l_i - l_0)   (sum in i order),
 // rounded to the activation dtype when out_bf16.
 // ---------------------------------------------------------------------------
+// Top-k of one token held by a wave (value descending, ties to the lower
+// expert index, as jax.lax.top_k), then w_j = expf(l_j - l_0) / sum_{i<K}
+// expf(l_i - l_0) (sum in j order). Lane owns experts lane + 64*i, i < EPL;
+// v[i] is the logit, -inf for NaN; entries past E are ignored.
+//
+// A radix select over order-preserving 32-bit keys (one ballot per bit and
+// experts-per-lane) finds the K-th largest key; the selected experts (keys
+// above it, then the lowest-index ties at it) are compacted into per-wave
+// LDS, each of the first K lanes ranks one of them against the others, and
+// the sorted list gives the outputs. -0.0 is keyed as +0.0 (they compare
+// equal). No wave-wide shuffles: ballots and scalar popcounts only.
+struct TopkLds {
+  uint32_t key[kMaxTopK];
+  int32_t idx[kMaxTopK];
+  float val[kMaxTopK];
+  int32_t sidx[kMaxTopK];
+};
+
+template <int EPL>
+__device__ __forceinline__ void wave_topk(int t, int E, int K, const float* v, int32_t* __restrict__ topk_idx,
+                                          float* __restrict__ topk_w, int out_bf16, int32_t* idx_lds, TopkLds& S) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  uint32_t key[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const float f = v[i] == 0.0f ? 0.0f : v[i];
+    const uint32_t u = __float_as_uint(f);
+    key[i] = (lane + 64 * i < E) ? ((u >> 31) ? ~u : (u | 0x80000000u)) : 0u;
+  }
+  uint32_t thr = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = thr | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) cnt += __popcll(__ballot(key[i] >= cand));
+    if (cnt >= K) thr = cand;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) gt += __popcll(__ballot(key[i] > thr));
+  const int need = K - gt;
+  int base_sel = 0, base_tie = 0;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const bool tie = key[i] == thr;
+    const unsigned long long mt = __ballot(tie);
+    const bool sel = key[i] > thr || (tie && base_tie + __popcll(mt & below) < need);
+    const unsigned long long ms = __ballot(sel);
+    if (sel) {
+      const int pos = base_sel + __popcll(ms & below);
+      S.key[pos] = key[i];
+      S.idx[pos] = lane + 64 * i;
+      S.val[pos] = v[i];
+    }
+    base_sel += __popcll(ms);
+    base_tie += __popcll(mt);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float my_v = 0.0f;
+  int my_i = 0, rank = 0;
+  if (lane < K) {
+    const uint32_t kj = S.key[lane];
+    my_i = S.idx[lane];
+    my_v = S.val[lane];
+    for (int m = 0; m < K; ++m) {
+      const uint32_t km = S.key[m];
+      rank += (km > kj) || (km == kj && S.idx[m] < my_i);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < K) {
+    S.sidx[rank] = my_i;
+    S.key[rank] = __float_as_uint(my_v);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < K) {
+    const float l0 = __uint_as_float(S.key[0]);
+    float ssum = 0.0f;
+    for (int j = 0; j < K; ++j) ssum = ssum + expf(__uint_as_float(S.key[j]) - l0);
+    const float p = expf(__uint_as_float(S.key[lane]) - l0) / ssum;
+    const int e = S.sidx[lane];
+    topk_w[(int64_t)t * K + lane] = out_bf16 ? round_bf16(p) : p;
+    topk_idx[(int64_t)t * K + lane] = e;
+    if (idx_lds) idx_lds[t * K + lane] = e;
+  }
+  // the LDS scratch is reused by this wave's next token
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <int TB, int EPL>
 struct Acc {
   float v[TB][EPL];
@@ -98,8 +196,12 @@ __global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int 
                                                  float* __restrict__ logits, int32_t* __restrict__ topk_idx,
                                                  float* __restrict__ topk_w, int out_bf16) {
   using Row = RouterRow<RT, EPL>;
-  // rows per prefetch stage: two stages of raw rows stay within 32 registers
-  constexpr int U0 = 16 / Row::kWords < 1 ? 1 : 16 / Row::kWords;
+  // rows per prefetch stage: a stage of raw rows is 32 registers for one
+  // token per block (latency-bound: a 64-row slice of a bf16 router takes 8
+  // dependent memory round trips), 16 registers otherwise (two stages and the
+  // accumulators fit the 128 registers of a 1024-thread block)
+  constexpr int RW = TB == 1 && G == 1 ? 32 : 16;
+  constexpr int U0 = RW / Row::kWords < 1 ? 1 : RW / Row::kWords;
   constexpr int U = U0 < 16 / TB ? U0 : 16 / TB;
   extern __shared__ float lds[];
   const int NWB = blockDim.x >> 6;
@@ -219,7 +321,9 @@ __global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int 
     __syncthreads();
   }
 
-  // top-k: lane owns experts lane + 64*i, i < EPL (E <= 64 * EPL)
+  // top-k: lane owns experts lane + 64*i, i < EPL (E <= 64 * EPL); the
+  // per-wave selection scratch sits after the partials
+  TopkLds* tk = reinterpret_cast<TopkLds*>(lds + (size_t)NWB * TE);
   for (int tt = w; tt < TB; tt += NWB) {
     const int t = t0 + tt;
     if (t >= T) break;
@@ -231,44 +335,14 @@ __global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int 
       v[i] = (e < E && q == q) ? q : -INFINITY;
       if (logits && e < E) logits[(int64_t)t * E + e] = q;
     }
-    uint32_t taken = 0;
-    float my_v = 0.0f;
-    int my_i = 0;
-    for (int j = 0; j < K; ++j) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-#pragma unroll
-      for (int i = 0; i < EPL; ++i) {
-        const int e = lane + 64 * i;
-        if (e < E && !((taken >> i) & 1u) && (v[i] > bv || bi == 0x7fffffff)) {
-          bv = v[i];
-          bi = e;
-        }
-      }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-      if (lane == j) {
-        my_v = bv;
-        my_i = bi;
-      }
-    }
-    const float m = __shfl(my_v, 0, 64);
-    const float ej = expf(my_v - m);
-    float ssum = 0.0f;
-    for (int j = 0; j < K; ++j) ssum = ssum + __shfl(ej, j, 64);
-    if (lane < K) {
-      const float p = ej / ssum;
-      topk_w[(int64_t)t * K + lane] = out_bf16 ? round_bf16(p) : p;
-      topk_idx[(int64_t)t * K + lane] = my_i;
-    }
+    if (E <= 128 || EPL < 4)
+      wave_topk<(EPL < 2 ? EPL : 2)>(t, E, K, v, topk_idx, topk_w, out_bf16, nullptr, tk[w]);
+    else if (E <= 256 || EPL < 8)
+      wave_topk<(EPL < 4 ? EPL : 4)>(t, E, K, v, topk_idx, topk_w, out_bf16, nullptr, tk[w]);
+    else if (E <= 512 || EPL < 16)
+      wave_topk<(EPL < 8 ? EPL : 8)>(t, E, K, v, topk_idx, topk_w, out_bf16, nullptr, tk[w]);
+    else
+      wave_topk<EPL>(t, E, K, v, topk_idx, topk_w, out_bf16, nullptr, tk[w]);
   }
 }
 
@@ -304,22 +378,25 @@ __global__ __launch_bounds__(256) void k_dispatch_count(int T, int E, int K, con
   for (int e = threadIdx.x; e < E; e += blockDim.x) hist[(int64_t)blockIdx.x * E + e] = __popcll(mask[e]);
 }
 
-// hist == nullptr: counts come from this block's masks (valid when T <= 64).
-__global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, int nblk,
-                                                           const int32_t* __restrict__ topk_idx,
-                                                           const int32_t* __restrict__ hist,
-                                                           int32_t* __restrict__ group_sizes,
-                                                           int32_t* __restrict__ offsets, int32_t* __restrict__ active,
-                                                           int32_t* __restrict__ sorted_token,
-                                                           int32_t* __restrict__ sorted_expert,
-                                                           int32_t* __restrict__ inv) {
-  __shared__ unsigned long long mask[kMaxExperts];
-  __shared__ int base[kMaxExperts];
-  __shared__ int wsum[4], wact[4];
-  __shared__ int red_tot[4 * 256], red_bef[4 * 256];
-  const int b = blockIdx.x;
+// The scatter for token chunk b. hist == nullptr: the counts come from this
+// chunk's masks (valid when T <= 64). idx may point to global memory or LDS.
+// Threads 0..255 do the work (blockDim.x >= 256, a multiple of 64); every
+// thread of the block must call it.
+struct DispatchLds {
+  unsigned long long mask[kMaxExperts];
+  int base[kMaxExperts];
+  int wsum[4], wact[4];
+  int red_tot[4 * 256], red_bef[4 * 256];
+};
+
+__device__ void dispatch_chunk(int T, int E, int K, int b, int nblk, const int32_t* idx,
+                               const int32_t* __restrict__ hist, int32_t* __restrict__ group_sizes,
+                               int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+                               int32_t* __restrict__ sorted_token, int32_t* __restrict__ sorted_expert,
+                               int32_t* __restrict__ inv, DispatchLds& L) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  chunk_masks(T, E, K, b, topk_idx, mask);
+  const bool wk = tid < 256;
+  chunk_masks(T, E, K, b, idx, L.mask);
 
   // this thread's experts: 4*tid .. 4*tid+3
   int tot[4], bef[4];
@@ -335,7 +412,7 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, i
     const int Q = (E + 3) >> 2, G = 256 / Q;
     const int q = tid % Q, gi = tid / Q;
     int pt[4] = {0, 0, 0, 0}, pb[4] = {0, 0, 0, 0};
-    if (gi < G) {
+    if (wk && gi < G) {
       const bool vec4 = (E & 3) == 0;
 #pragma unroll 4
       for (int bb = gi; bb < nblk; bb += G) {
@@ -355,25 +432,27 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, i
         }
       }
     }
+    if (wk) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      red_tot[i * 256 + tid] = pt[i];
-      red_bef[i * 256 + tid] = pb[i];
+      for (int i = 0; i < 4; ++i) {
+        L.red_tot[i * 256 + tid] = pt[i];
+        L.red_bef[i * 256 + tid] = pb[i];
+      }
     }
     __syncthreads();
     if (tid < Q) {
       for (int g = 0; g < G; ++g) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          tot[i] += red_tot[i * 256 + g * Q + tid];
-          bef[i] += red_bef[i * 256 + g * Q + tid];
+          tot[i] += L.red_tot[i * 256 + g * Q + tid];
+          bef[i] += L.red_bef[i * 256 + g * Q + tid];
         }
       }
     }
-  } else {
+  } else if (wk) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (4 * tid + i < E) tot[i] = __popcll(mask[4 * tid + i]);
+      if (4 * tid + i < E) tot[i] = __popcll(L.mask[4 * tid + i]);
   }
   int lsum = 0, lact = 0;
 #pragma unroll
@@ -392,33 +471,35 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, i
       iact += va;
     }
   }
-  if (lane == 63) {
-    wsum[wv] = isum;
-    wact[wv] = iact;
+  if (wk && lane == 63) {
+    L.wsum[wv] = isum;
+    L.wact[wv] = iact;
   }
   __syncthreads();
-  int run = isum - lsum, arun = iact - lact;
-  for (int q = 0; q < wv; ++q) {
-    run += wsum[q];
-    arun += wact[q];
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = 4 * tid + i;
-    if (e < E) {
-      if (b == 0) {
-        group_sizes[e] = tot[i];
-        offsets[e] = run;
-        if (tot[i] > 0) active[arun] = e;
-      }
-      base[e] = run + bef[i];
+  if (wk) {
+    int run = isum - lsum, arun = iact - lact;
+    for (int q = 0; q < wv; ++q) {
+      run += L.wsum[q];
+      arun += L.wact[q];
     }
-    run += tot[i];
-    arun += tot[i] > 0;
-  }
-  if (b == 0 && tid == 255) {
-    offsets[E] = run;
-    active[E] = arun;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 4 * tid + i;
+      if (e < E) {
+        if (b == 0) {
+          group_sizes[e] = tot[i];
+          offsets[e] = run;
+          if (tot[i] > 0) active[arun] = e;
+        }
+        L.base[e] = run + bef[i];
+      }
+      run += tot[i];
+      arun += tot[i] > 0;
+    }
+    if (b == 0 && tid == 255) {
+      offsets[E] = run;
+      active[E] = arun;
+    }
   }
   __syncthreads();
 
@@ -427,11 +508,11 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, i
   const int M = T * K;
   for (int m = tid; m < n; m += blockDim.x) {
     const int tl = m / K;
-    const int e = topk_idx[(int64_t)t0 * K + m];
+    const int e = idx[(int64_t)t0 * K + m];
     // indices outside [0, E) or counts that disagree with them are caller errors
     // of the stage entry point; they are skipped rather than written out of bounds
     if ((unsigned)e < (unsigned)E) {
-      const int p = base[e] + __popcll(mask[e] & ((1ull << tl) - 1ull));
+      const int p = L.base[e] + __popcll(L.mask[e] & ((1ull << tl) - 1ull));
       if ((unsigned)p < (unsigned)M) {
         sorted_token[p] = t0 + tl;
         sorted_expert[p] = e;
@@ -439,6 +520,19 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, i
       }
     }
   }
+}
+
+__global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, int nblk,
+                                                           const int32_t* __restrict__ topk_idx,
+                                                           const int32_t* __restrict__ hist,
+                                                           int32_t* __restrict__ group_sizes,
+                                                           int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+                                                           int32_t* __restrict__ sorted_token,
+                                                           int32_t* __restrict__ sorted_expert,
+                                                           int32_t* __restrict__ inv) {
+  __shared__ DispatchLds L;
+  dispatch_chunk(T, E, K, blockIdx.x, nblk, topk_idx, hist, group_sizes, offsets, active, sorted_token, sorted_expert,
+                 inv, L);
 }
 
 }  // namespace kmoe
@@ -474,10 +568,11 @@ static RouteShape route_shape(const kmoe_desc& d) {
   int tb = 8;
   const int acc_cap = r.G > 1 ? 2 * r.EPL : 64;
   auto x_bytes = [&](int t) { return (size_t)4 * r.S * (kRouterSlice * t + 4); };
-  while (tb > 1 && (tb * r.EPL > acc_cap || x_bytes(tb) > 65536 || (size_t)r.NWB * tb * E * 4 > 65536)) tb >>= 1;
+  auto part_bytes = [&](int t) { return (size_t)4 * r.NWB * t * E + r.NWB * sizeof(TopkLds); };
+  while (tb > 1 && (tb * r.EPL > acc_cap || x_bytes(tb) > 65536 || part_bytes(tb) > 65536)) tb >>= 1;
   while (tb > 1 && (T + tb - 1) / tb < 256) tb >>= 1;
   r.TB = tb;
-  r.lds = std::max(x_bytes(tb), (size_t)4 * r.NWB * tb * E);
+  r.lds = std::max(x_bytes(tb), part_bytes(tb));
   return r;
 }
 
