@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define KMOE_ABI_VERSION 1
+#define KMOE_ABI_VERSION 2
 
 typedef enum kmoe_status {
   KMOE_OK = 0,
@@ -82,6 +82,12 @@ typedef struct kmoe_desc {
   kmoe_dtype act_dtype;           /* F32 or BF16 (x.dtype)                     */
   int64_t decode_token_threshold; /* T <= this uses the decode kernels
                                      (moe_ragged_decode_token_threshold, :49) */
+  int64_t expert_capacity;        /* 0: dropless (gather_einsum / ragged paths).
+                                     > 0: fixed_capacity token dropping: an assignment
+                                     whose slot within its expert's stable order is
+                                     >= this is dropped and adds nothing to its
+                                     token's output (kappa/qwen3/ffn_moe.py:107-158;
+                                     the caller passes min(c_dyn, c_buf), :136-141) */
 } kmoe_desc;
 
 /* W8 expert weights relaid out once, at load time, for the gfx950 kernels

@@ -72,6 +72,7 @@ class KmoeDesc(ctypes.Structure):
         ("intermediate", ctypes.c_int64),
         ("act_dtype", ctypes.c_int),
         ("decode_token_threshold", ctypes.c_int64),
+        ("expert_capacity", ctypes.c_int64),
     ]
 
 

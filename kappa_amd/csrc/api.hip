@@ -57,6 +57,8 @@ kmoe_status check_desc(const kmoe_desc* d) {
                 kmoe::kRouterSlice * kmoe::kMaxRouterSlices);
   if (d->tokens * d->top_k > (int64_t)0x7fffffff || d->tokens * d->hidden > ((int64_t)1 << 40))
     return fail(KMOE_ERR_UNSUPPORTED, "tokens %lld too large", (long long)d->tokens);
+  if (d->expert_capacity < 0)
+    return fail(KMOE_ERR_INVALID_ARG, "expert_capacity must be >= 0 (got %lld)", (long long)d->expert_capacity);
   return KMOE_OK;
 }
 

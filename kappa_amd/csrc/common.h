@@ -63,6 +63,11 @@ __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; 
 // Host-side helpers shared by the launch wrappers.
 namespace kmoe_host {
 
+// Rows an expert keeps: the fixed_capacity slot limit, or no limit.
+inline int capacity_of(const kmoe_desc& d) {
+  return d.expert_capacity > 0 && d.expert_capacity < 0x7fffffff ? (int)d.expert_capacity : 0x7fffffff;
+}
+
 inline size_t dtype_size(kmoe_dtype t) {
   switch (t) {
     case KMOE_DTYPE_F32:

@@ -48,11 +48,11 @@ __device__ __forceinline__ floatx4 mfma16(const bf16x8 a, const bf16x8 b, const 
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// Block-wide tile prefix over experts: mtp[e] = sum_{e' < e} ceil(group_size[e'] / BM), mtp[E] = total.
+// Block-wide tile prefix over experts: mtp[e] = sum_{e' < e} ceil(min(group_size[e'], cap) / BM), mtp[E] = total.
 // The first 256 threads compute it (E <= 1024); blockDim.x must be a multiple of 64, at least 256.
 // wsum: 4 ints of LDS scratch.
 template <int BM>
-__device__ void tile_prefix(const int32_t* __restrict__ offsets, int E, int* mtp, int* wsum) {
+__device__ void tile_prefix(const int32_t* __restrict__ offsets, int E, int cap, int* mtp, int* wsum) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   int c[4];
   int local = 0, incl = 0;
@@ -61,7 +61,7 @@ __device__ void tile_prefix(const int32_t* __restrict__ offsets, int E, int* mtp
     for (int i = 0; i < 4; ++i) {
       const int e = tid * 4 + i;
       c[i] = 0;
-      if (e < E) c[i] = (offsets[e + 1] - offsets[e] + BM - 1) / BM;
+      if (e < E) c[i] = (min(offsets[e + 1] - offsets[e], cap) + BM - 1) / BM;
       local += c[i];
     }
     incl = local;
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int D, int I, int E, cons
                                                         const int32_t* __restrict__ active,
                                                         const int32_t* __restrict__ sorted_token,
                                                         const int8_t* __restrict__ w13, const float* __restrict__ s13,
-                                                        uint16_t* __restrict__ h_sorted) {
+                                                        uint16_t* __restrict__ h_sorted, int cap) {
   __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][kDecodeMaxRowBlocks][2][64];
   const int ig = blockIdx.x;
   const int slot = blockIdx.y;
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int D, int I, int E, cons
   const float sg = s13[(((size_t)e * IG + ig) * 2 + 0) * 16 + (lane & 15)];
   const float su = s13[(((size_t)e * IG + ig) * 2 + 1) * 16 + (lane & 15)];
   const int r0 = offsets[e];
-  const int nrows = offsets[e + 1] - r0;
+  const int nrows = min(offsets[e + 1] - r0, cap);
   const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
   const int koff = 16 * (lane >> 4);
   const uint16_t* xr[kDecodeMaxRowBlocks];
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
                                                       const int32_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ active,
                                                       const int8_t* __restrict__ w2, const float* __restrict__ s2,
-                                                      uint16_t* __restrict__ y_sorted) {
+                                                      uint16_t* __restrict__ y_sorted, int cap) {
   __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][kDecodeMaxRowBlocks][NCG][64];
   const int dt = blockIdx.x;  // NCG*16 output columns
   const int slot = blockIdx.y;
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) sc[cg] = s2[(size_t)e * D + (dt * NCG + cg) * 16 + (lane & 15)];
   const int r0 = offsets[e];
-  const int nrows = offsets[e + 1] - r0;
+  const int nrows = min(offsets[e + 1] - r0, cap);
   const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
   const int koff = 16 * (lane >> 4);
   const uint16_t* hr[kDecodeMaxRowBlocks];
@@ -345,9 +345,9 @@ struct PrefillLds {
   int wsum[4];
 };
 
-__device__ __forceinline__ bool prefill_tile(const int32_t* __restrict__ offsets, int E, int NT, PrefillLds& s,
+__device__ __forceinline__ bool prefill_tile(const int32_t* __restrict__ offsets, int E, int NT, int cap, PrefillLds& s,
                                              int& e, int& row0, int& rows, int& nt) {
-  tile_prefix<kBM>(offsets, E, s.mtp, s.wsum);
+  tile_prefix<kBM>(offsets, E, cap, s.mtp, s.wsum);
   const int ntiles = s.mtp[E] * NT;
   const int per = (ntiles + 7) >> 3;
   const int q = blockIdx.x >> 3;
@@ -359,7 +359,7 @@ __device__ __forceinline__ bool prefill_tile(const int32_t* __restrict__ offsets
   e = tile_expert(s.mtp, E, mt_glob);
   const int mt = mt_glob - s.mtp[e];
   row0 = offsets[e] + mt * kBM;
-  rows = min(kBM, offsets[e + 1] - row0);
+  rows = min(kBM, offsets[e] + min(offsets[e + 1] - offsets[e], cap) - row0);
   return true;
 }
 
@@ -371,14 +371,14 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
                                                      const int32_t* __restrict__ offsets,
                                                      const int32_t* __restrict__ sorted_token,
                                                      const int8_t* __restrict__ wp, const float* __restrict__ sp,
-                                                     uint16_t* __restrict__ dst) {
+                                                     uint16_t* __restrict__ dst, int cap) {
   __shared__ PrefillLds s;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int Kdim = GATEUP ? D : I;
   const int Ndim = GATEUP ? I : D;
   const int NT = GATEUP ? (I >> 6) : (D >> 7);
   int e, row0, rows, nt;
-  if (!prefill_tile(offsets, E, NT, s, e, row0, rows, nt)) return;
+  if (!prefill_tile(offsets, E, NT, cap, s, e, row0, rows, nt)) return;
   if (tid < kBM) s.tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
   __syncthreads();
 
@@ -672,7 +672,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
                                                   const int32_t* __restrict__ offsets,
                                                   const int32_t* __restrict__ sorted_token,
                                                   const int8_t* __restrict__ wp, const float* __restrict__ sp,
-                                                  uint16_t* __restrict__ dst) {
+                                                  uint16_t* __restrict__ dst, int cap) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kGemmLds];
   // set-up scratch inside the ring (no loads are in flight yet)
   int* const mtp = reinterpret_cast<int*>(smem);
@@ -680,7 +680,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   int* const wsum = tok + kGemmRows;
   const int tid = threadIdx.x, lane = tid & 63;
   const int NT = GATEUP ? I / 128 : D / 256;
-  tile_prefix<kGemmRows>(offsets, E, mtp, wsum);
+  tile_prefix<kGemmRows>(offsets, E, cap, mtp, wsum);
   const int ntiles = mtp[E] * NT;
   const int per = (ntiles + 7) >> 3;
   const int q = blockIdx.x >> 3;
@@ -694,7 +694,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   const int nt = __builtin_amdgcn_readfirstlane(rem / nmt_e);
   const int mt = rem - nt * nmt_e;
   const int row0 = __builtin_amdgcn_readfirstlane(offsets[e] + mt * kGemmRows);
-  const int rows = __builtin_amdgcn_readfirstlane(min(kGemmRows, offsets[e + 1] - row0));
+  const int rows =
+      __builtin_amdgcn_readfirstlane(min(kGemmRows, offsets[e] + min(offsets[e + 1] - offsets[e], cap) - row0));
   if (tid < kGemmRows) tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
   __syncthreads();
 
@@ -856,16 +857,20 @@ __global__ __launch_bounds__(256) void k_combine8(int T, int K, int D, const A* 
   for (int jb = 0; jb < K; jb += 8) {
     const int nj = min(8, K - jb);
     float wj[8], yv[8][8];
+    bool on[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      if (j < nj) {
+      // a dropped assignment (inv < 0, fixed_capacity) adds nothing
+      const int p = j < nj ? inv[(int64_t)t * K + jb + j] : -1;
+      on[j] = p >= 0;
+      if (on[j]) {
         wj[j] = w[(int64_t)t * K + jb + j];
-        Vec8<A>::load(y + (int64_t)inv[(int64_t)t * K + jb + j] * D + n0, yv[j]);
+        Vec8<A>::load(y + (int64_t)p * D + n0, yv[j]);
       }
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (j < nj)
+      if (on[j])
 #pragma unroll
         for (int v = 0; v < 8; ++v) acc[v] = __builtin_fmaf(wj[j], yv[j][v], acc[v]);
   }
@@ -881,8 +886,10 @@ __global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* 
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= D) return;
   float acc = 0.0f;
-  for (int j = 0; j < K; ++j)
-    acc = __builtin_fmaf(w[(int64_t)t * K + j], Act<A>::load(y, (int64_t)inv[(int64_t)t * K + j] * D + n), acc);
+  for (int j = 0; j < K; ++j) {
+    const int p = inv[(int64_t)t * K + j];
+    if (p >= 0) acc = __builtin_fmaf(w[(int64_t)t * K + j], Act<A>::load(y, (int64_t)p * D + n), acc);
+  }
   Act<A>::store(out, (int64_t)t * D + n, acc);
 }
 
@@ -906,6 +913,7 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
             I = (int)d.intermediate;
   const int M = T * K;
   const int slots = M < E ? M : E;
+  const int cap = capacity_of(d);
   const uint16_t* xb = reinterpret_cast<const uint16_t*>(x);
   uint16_t* hb = reinterpret_cast<uint16_t*>(h_sorted);
   uint16_t* yb = reinterpret_cast<uint16_t*>(y_sorted);
@@ -921,10 +929,10 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
       const dim3 grid(I / 16, slots);
       if ((D / 64) % 4 == 0 && cpw % 4 == 0)
         hipLaunchKernelGGL((k_gateup_decode<4, 4, false>), grid, dim3(256), 0, st, D, I, E, xb, offsets, active,
-                           sorted_token, w13, s13, hb);
+                           sorted_token, w13, s13, hb, cap);
       else
         hipLaunchKernelGGL((k_gateup_decode<4, 4, true>), grid, dim3(256), 0, st, D, I, E, xb, offsets, active,
-                           sorted_token, w13, s13, hb);
+                           sorted_token, w13, s13, hb, cap);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
     }
@@ -933,10 +941,10 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
       const dim3 grid(D / 32, slots);
       if ((I / 64) % 4 == 0 && cpw % 3 == 0)
         hipLaunchKernelGGL((k_down_decode<4, 2, 3, false>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
-                           s2, yb);
+                           s2, yb, cap);
       else
         hipLaunchKernelGGL((k_down_decode<4, 2, 4, true>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
-                           s2, yb);
+                           s2, yb, cap);
       return hipGetLastError();
     }
     return hipSuccess;
@@ -948,13 +956,13 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
     auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };
     if (stages & kStageGateUp) {
       hipLaunchKernelGGL((k_gemm<true>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb, offsets,
-                         sorted_token, w13, s13, hb);
+                         sorted_token, w13, s13, hb, cap);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
     }
     if (stages & kStageDown) {
       hipLaunchKernelGGL((k_gemm<false>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb, offsets,
-                         sorted_token, w2, s2, yb);
+                         sorted_token, w2, s2, yb, cap);
       return hipGetLastError();
     }
     return hipSuccess;
@@ -966,13 +974,13 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
   };
   if (stages & kStageGateUp) {
     hipLaunchKernelGGL((k_prefill<true>), dim3(grid_for(I / 64)), dim3(256), 0, st, D, I, E, xb, offsets,
-                       sorted_token, w13, s13, hb);
+                       sorted_token, w13, s13, hb, cap);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   if (stages & kStageDown) {
     hipLaunchKernelGGL((k_prefill<false>), dim3(grid_for(D / 128)), dim3(256), 0, st, D, I, E, hb, offsets,
-                       sorted_token, w2, s2, yb);
+                       sorted_token, w2, s2, yb, cap);
     return hipGetLastError();
   }
   return hipSuccess;

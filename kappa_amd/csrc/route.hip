@@ -380,11 +380,14 @@ __global__ __launch_bounds__(256) void k_dispatch_count(int T, int E, int K, con
 
 // The scatter for token chunk b. hist == nullptr: the counts come from this
 // chunk's masks (valid when T <= 64). idx may point to global memory or LDS.
+// An assignment whose slot within its expert (sorted position - the expert's
+// offset) is >= cap is dropped: inv = -1 (fixed_capacity).
 // Threads 0..255 do the work (blockDim.x >= 256, a multiple of 64); every
 // thread of the block must call it.
 struct DispatchLds {
   unsigned long long mask[kMaxExperts];
   int base[kMaxExperts];
+  int start[kMaxExperts];
   int wsum[4], wact[4];
   int red_tot[4 * 256], red_bef[4 * 256];
 };
@@ -393,7 +396,7 @@ __device__ void dispatch_chunk(int T, int E, int K, int b, int nblk, const int32
                                const int32_t* __restrict__ hist, int32_t* __restrict__ group_sizes,
                                int32_t* __restrict__ offsets, int32_t* __restrict__ active,
                                int32_t* __restrict__ sorted_token, int32_t* __restrict__ sorted_expert,
-                               int32_t* __restrict__ inv, DispatchLds& L) {
+                               int32_t* __restrict__ inv, int cap, DispatchLds& L) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const bool wk = tid < 256;
   chunk_masks(T, E, K, b, idx, L.mask);
@@ -492,6 +495,7 @@ __device__ void dispatch_chunk(int T, int E, int K, int b, int nblk, const int32
           if (tot[i] > 0) active[arun] = e;
         }
         L.base[e] = run + bef[i];
+        L.start[e] = run;
       }
       run += tot[i];
       arun += tot[i] > 0;
@@ -516,7 +520,7 @@ __device__ void dispatch_chunk(int T, int E, int K, int b, int nblk, const int32
       if ((unsigned)p < (unsigned)M) {
         sorted_token[p] = t0 + tl;
         sorted_expert[p] = e;
-        inv[(int64_t)t0 * K + m] = p;
+        inv[(int64_t)t0 * K + m] = p - L.start[e] < cap ? p : -1;
       }
     }
   }
@@ -529,10 +533,10 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, i
                                                            int32_t* __restrict__ offsets, int32_t* __restrict__ active,
                                                            int32_t* __restrict__ sorted_token,
                                                            int32_t* __restrict__ sorted_expert,
-                                                           int32_t* __restrict__ inv) {
+                                                           int32_t* __restrict__ inv, int cap) {
   __shared__ DispatchLds L;
   dispatch_chunk(T, E, K, blockIdx.x, nblk, topk_idx, hist, group_sizes, offsets, active, sorted_token, sorted_expert,
-                 inv, L);
+                 inv, cap, L);
 }
 
 }  // namespace kmoe
@@ -650,7 +654,7 @@ hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const in
   const int nblk = (T + kDispatchBlock - 1) / kDispatchBlock;
   if (!hist && nblk > 1) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_dispatch_scatter, dim3(nblk), dim3(256), 0, st, T, E, K, nblk, topk_idx, hist, group_sizes,
-                     offsets, active, sorted_token, sorted_expert, inv);
+                     offsets, active, sorted_token, sorted_expert, inv, capacity_of(d));
   return hipGetLastError();
 }
 

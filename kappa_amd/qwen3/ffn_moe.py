@@ -16,10 +16,12 @@ every kernel family follows the same numerics, so the choice only affects speed.
 
 from __future__ import annotations
 
+import math
 import threading
 from collections import OrderedDict
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -27,6 +29,30 @@ from .architecture import Qwen3Config
 from .quant import Q8Weight, Weight, is_q8_weight, kmoe_dtype, weight_struct
 
 _MOE_IMPLS = ("gather_einsum", "fixed_capacity", "ragged_jax", "ragged_tokamax")
+
+# Upper bound on B*T when deriving the static fixed_capacity buffer depth
+# (kappa/qwen3/ffn_moe.py:20).
+_MOE_FIXED_CAP_MAX_BT = 8192
+
+
+def _fixed_capacity_buffer_slots(cfg: Qwen3Config) -> int:
+    """Static per-expert buffer depth c_buf (kappa/qwen3/ffn_moe.py:23-31)."""
+    if cfg.moe_fixed_capacity_slots is not None:
+        return max(1, int(cfg.moe_fixed_capacity_slots))
+    k, e = cfg.num_experts_per_tok, cfg.num_experts
+    if e <= 0 or k <= 0:
+        return 1
+    cap = cfg.moe_capacity_factor * _MOE_FIXED_CAP_MAX_BT * k / e
+    return max(1, int(math.ceil(cap)))
+
+
+def _fixed_capacity(cfg: Qwen3Config, total_tokens: int) -> int:
+    """Slot limit min(c_dyn, c_buf): c_dyn = max(1, round(f32(cf) * f32(B*T*K) / f32(E)))
+    in float32 with round-half-even (kappa/qwen3/ffn_moe.py:136-141)."""
+    k, e = cfg.num_experts_per_tok, cfg.num_experts
+    prod = np.float32(cfg.moe_capacity_factor) * np.float32(total_tokens * k)
+    c_dyn = max(1, int(np.round(np.float32(prod / np.float32(e)))))
+    return min(c_dyn, _fixed_capacity_buffer_slots(cfg))
 
 
 def _expert_count(w: Weight) -> int:
@@ -62,8 +88,11 @@ class PackedExperts:
         return _lib.KmoePacked(self.w13.data_ptr(), self.s13.data_ptr(), self.w2.data_ptr(), self.s2.data_ptr())
 
 
-def _desc(T: int, D: int, E: int, K: int, I: int, act: torch.dtype, threshold: int) -> _lib.KmoeDesc:
-    return _lib.KmoeDesc(T, D, E, K, I, kmoe_dtype(act), threshold)
+def _desc(
+    T: int, D: int, E: int, K: int, I: int, act: torch.dtype, threshold: int, capacity: int = 0
+) -> _lib.KmoeDesc:
+    """kmoe_desc; capacity 0 is dropless, > 0 the fixed_capacity slot limit."""
+    return _lib.KmoeDesc(T, D, E, K, I, kmoe_dtype(act), threshold, capacity)
 
 
 def _stream(device: torch.device) -> int:
@@ -181,6 +210,7 @@ def _moe_forward(
     decode_threshold: int,
     packed: PackedExperts | None,
     return_routing: bool = False,
+    capacity: int = 0,
 ):
     b, t, d = _route_checks(x, router_w, num_experts)
     if x.device.type != "cuda":
@@ -199,7 +229,7 @@ def _moe_forward(
     dev = x.device
     T = b * t
     x_flat = x.reshape(T, d).contiguous()
-    desc = _desc(T, d, E, K, I, x.dtype, decode_threshold)
+    desc = _desc(T, d, E, K, I, x.dtype, decode_threshold, capacity)
     r, kr = weight_struct(router_w, dev, n_out=E, n_groups=None, name="router_w")
     if packed is None and packable(x.dtype, ffn_gate, ffn_up, ffn_down):
         packed = PACK_CACHE.get(ffn_gate, ffn_up, ffn_down)
@@ -255,15 +285,18 @@ def moe_swiglu_ffn(
     impl = _effective_moe_impl(cfg, total_tokens=b * t)
     if impl not in _MOE_IMPLS:
         raise ValueError(f"unknown moe_impl: {impl!r}")
+    capacity = 0
     if impl == "fixed_capacity":
         if cfg.moe_capacity_factor <= 0:
             raise ValueError("fixed_capacity requires cfg.moe_capacity_factor > 0")
-        raise NotImplementedError("moe_impl='fixed_capacity' (token dropping) is not implemented on MI355X yet")
+        # token dropping: the dropless kernels with each expert limited to its
+        # first `capacity` assignments in the stable (expert, token) order
+        capacity = _fixed_capacity(cfg, b * t)
     # gather_einsum, ragged_jax and ragged_tokamax are dropless and share one numerics contract here.
     return _moe_forward(
         x, router_w, ffn_gate, ffn_up, ffn_down,
         num_experts=cfg.num_experts, num_experts_per_tok=cfg.num_experts_per_tok,
-        decode_threshold=cfg.moe_ragged_decode_token_threshold, packed=packed,
+        decode_threshold=cfg.moe_ragged_decode_token_threshold, packed=packed, capacity=capacity,
     )  # fmt: skip
 
 

@@ -35,12 +35,14 @@ def route(x_flat: torch.Tensor, router_w: Weight, *, num_experts: int, k: int) -
     return {"logits": logits, "idx": idx, "w": w, "hist": hist}
 
 
-def dispatch(idx: torch.Tensor, hist: torch.Tensor, *, num_experts: int) -> dict:
-    """Stable sort of the (t, j) assignments by expert."""
+def dispatch(idx: torch.Tensor, hist: torch.Tensor, *, num_experts: int, capacity: int = 0) -> dict:
+    """Stable sort of the (t, j) assignments by expert. capacity > 0
+    (fixed_capacity): inv is -1 for an assignment whose slot within its expert
+    is >= capacity."""
     T, k = idx.shape
     dev = idx.device
     M = T * k
-    desc = _desc(T, 1, num_experts, k, 1, torch.float32, 0)
+    desc = _desc(T, 1, num_experts, k, 1, torch.float32, 0, capacity)
     out = {
         "group_sizes": torch.empty(num_experts, dtype=torch.int32, device=dev),
         "offsets": torch.empty(num_experts + 1, dtype=torch.int32, device=dev),
@@ -70,16 +72,19 @@ def expert_ffn(
     decode_threshold: int = 64,
     packed: PackedExperts | None = None,
     layout_native: bool = False,
+    capacity: int = 0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """SwiGLU experts over the sorted rows: (h_sorted [M, I], y_sorted [M, D]) in x.dtype.
 
     ``layout_native=True`` runs the kernels that read the reference layout
-    directly (one fmaf chain per output) instead of the packed MFMA kernels."""
+    directly (one fmaf chain per output) instead of the packed MFMA kernels.
+    ``capacity > 0``: the packed kernels compute only each expert's first
+    ``capacity`` rows (the others are left as they were)."""
     T, D = x_flat.shape
     E, _, I = _shape(ffn_gate)
     dev = x_flat.device
     M = T * k
-    desc = _desc(T, D, E, k, I, x_flat.dtype, decode_threshold)
+    desc = _desc(T, D, E, k, I, x_flat.dtype, decode_threshold, capacity)
     if not layout_native and packed is None and packable(x_flat.dtype, ffn_gate, ffn_up, ffn_down):
         packed = PACK_CACHE.get(ffn_gate, ffn_up, ffn_down)
     if layout_native:

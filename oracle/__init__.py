@@ -19,13 +19,17 @@ Function -> reference it restates:
   dispatch        kappa/qwen3/ffn_moe.py:189-200, 212 (argsort stable, bincount, inv)
   expert_ffn      kappa/qwen3/ffn_moe.py:99-102 with kappa/qwen3/quant.py:60-76
   combine         kappa/qwen3/ffn_moe.py:103, 214-215
-  forward         kappa/qwen3/ffn_moe.py:226-299 (moe_swiglu_ffn, dropless paths)
+  forward         kappa/qwen3/ffn_moe.py:226-299 (moe_swiglu_ffn; capacity= gives
+                  the fixed_capacity path, :107-158)
+  capacity_slots  kappa/qwen3/ffn_moe.py:23-31, 136-141 (c_buf and c_dyn)
+  drop_over_capacity  kappa/qwen3/ffn_moe.py:59-71, 141, 153 (slot within expert, mask)
   quantize_*      kappa/qwen3/quant.py:41-48
 """
 
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 import subprocess
 from typing import Any
@@ -190,12 +194,43 @@ def combine(y_sorted, inv, w, act_bf16: bool) -> np.ndarray:
     return out
 
 
-def forward(x, router, gate, up, down, *, k: int, act_bf16: bool) -> dict:
-    """Whole block on flattened tokens x [T, D]; returns every intermediate."""
+def capacity_slots(T: int, K: int, E: int, capacity_factor: float, fixed_slots: int | None = None) -> int:
+    """fixed_capacity slot limit min(c_dyn, c_buf) for T flattened tokens.
+
+    c_buf is the static buffer depth (kappa/qwen3/ffn_moe.py:23-31, with the
+    8192-token bound of :20); c_dyn = max(1, round_half_even(f32(cf) *
+    f32(T*K) / f32(E))) in float32 arithmetic (:136-139)."""
+    if fixed_slots is not None:
+        c_buf = max(1, int(fixed_slots))
+    elif E <= 0 or K <= 0:
+        c_buf = 1
+    else:
+        c_buf = max(1, int(math.ceil(capacity_factor * 8192 * K / E)))
+    prod = np.float32(capacity_factor) * np.float32(T * K)
+    c_dyn = max(1, int(np.round(np.float32(prod / np.float32(E)))))
+    return min(c_dyn, c_buf)
+
+
+def drop_over_capacity(idx, disp: dict, capacity: int) -> np.ndarray:
+    """inv with -1 for each assignment whose slot within its expert (position in
+    the stable order minus the expert's offset) is >= capacity."""
+    idx = np.asarray(idx, np.int32).reshape(-1)
+    inv = np.asarray(disp["inv"], np.int32).copy()
+    slot = inv - np.asarray(disp["offsets"], np.int32)[idx]
+    inv[slot >= capacity] = -1
+    return inv
+
+
+def forward(x, router, gate, up, down, *, k: int, act_bf16: bool, capacity: int | None = None) -> dict:
+    """Whole block on flattened tokens x [T, D]; returns every intermediate.
+
+    capacity: None for the dropless paths, else the fixed_capacity slot limit."""
     logits = router_logits(x, router)
     E = logits.shape[1]
     idx, w = topk_softmax(logits, k, act_bf16)
     disp = dispatch(idx, E)
+    if capacity is not None:
+        disp["inv"] = drop_over_capacity(idx, disp, capacity)
     h, y = expert_ffn(x, disp["offsets"], disp["sorted_token"], gate, up, down, act_bf16)
     out = combine(y, disp["inv"], w, act_bf16)
     return {"logits": logits, "idx": idx, "w": w, **disp, "h_sorted": h, "y_sorted": y, "out": out}

@@ -294,7 +294,12 @@ void orc_combine(int64_t T, int64_t K, int64_t D, int round_bf16, const float* y
   for (int64_t t = 0; t < T; ++t) {
     for (int64_t n = 0; n < D; ++n) {
       float acc = 0.0f;
-      for (int64_t j = 0; j < K; ++j) acc = fmaf(w[t * K + j], y_sorted[(int64_t)inv[t * K + j] * D + n], acc);
+      for (int64_t j = 0; j < K; ++j) {
+        /* inv < 0: an assignment dropped by fixed_capacity adds nothing
+         * (kappa/qwen3/ffn_moe.py:153, y_pick = 0) */
+        if (inv[t * K + j] < 0) continue;
+        acc = fmaf(w[t * K + j], y_sorted[(int64_t)inv[t * K + j] * D + n], acc);
+      }
       out[t * D + n] = round_bf16 ? bf16r(acc) : acc;
     }
   }

@@ -152,3 +152,13 @@ GOLDEN_SPECS = [
     Spec("tie_zero_x", T=4, D=64, E=8, K=3, I=32, x_zero=True, base_seed=50),
     Spec("tie_router", T=8, D=64, E=8, K=3, I=32, tie_router=True, base_seed=60),
 ]
+
+# fixed_capacity cases (kappa/qwen3/ffn_moe.py:107-158): (spec, capacity_factor, moe_fixed_capacity_slots)
+#   cap_w8c_bf16:   c_dyn = round(0.5 * 128 / 16) = 4 slots for ~8 assignments per expert
+#   cap_f32_slots:  c_dyn = round(1.25 * 48 / 8) = 8, capped by 3 static slots (c_buf)
+#   cap_skew_bf16:  Zipf-skewed routing, c_dyn = 6: the hot experts overflow
+CAPACITY_SPECS = [
+    (Spec("cap_w8c_bf16", T=32, D=128, E=16, K=4, I=64, base_seed=70), 0.5, None),
+    (Spec("cap_f32_slots", T=24, D=64, E=8, K=2, I=32, act="f32", weights="f32", router="f32", base_seed=80), 1.25, 3),
+    (Spec("cap_skew_bf16", T=48, D=128, E=16, K=2, I=64, skew_lambda=1.0, base_seed=90), 1.0, None),
+]

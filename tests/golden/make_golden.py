@@ -10,6 +10,8 @@ checked against an independent restatement:
   moe_take_dequant  kappa/qwen3/quant.py:60-76
   _moe_gather_einsum kappa/qwen3/ffn_moe.py:74-104 (the default path)
   _moe_ragged order  kappa/qwen3/ffn_moe.py:189-200, 212 (argsort stable, bincount, inv)
+  _moe_fixed_capacity kappa/qwen3/ffn_moe.py:107-158 with _slot_within_expert :59-71
+                     and _fixed_capacity_buffer_slots :23-31 (token dropping)
 
 Accumulations run in float64 and are rounded to the activation dtype at the
 points where the reference's arrays carry ``x.dtype``; bf16 rounding uses
@@ -30,7 +32,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
-from inputs import GOLDEN_SPECS, Spec, digest, make_inputs  # noqa: E402
+from inputs import CAPACITY_SPECS, GOLDEN_SPECS, Spec, digest, make_inputs  # noqa: E402
 
 
 def as_act(a, act: str) -> np.ndarray:
@@ -117,6 +119,68 @@ def reference_block(spec: Spec, inp: dict) -> dict:
     }
 
 
+def fixed_capacity_slots(T: int, K: int, E: int, cf: float, fixed_slots) -> tuple:
+    """(c_dyn, c_buf): c_buf as kappa/qwen3/ffn_moe.py:23-31 (8192-token bound, :20);
+    c_dyn = max(1, round(f32(cf) * f32(T*K) / f32(E))) in float32 (:136-139)."""
+    import math
+
+    if fixed_slots is not None:
+        c_buf = max(1, int(fixed_slots))
+    else:
+        c_buf = max(1, int(math.ceil(cf * 8192 * K / E)))
+    c_dyn = max(1, int(np.round(np.float32(np.float32(cf) * np.float32(T * K)) / np.float32(E))))
+    return c_dyn, c_buf
+
+
+def reference_fixed_capacity(spec: Spec, inp: dict, blk: dict, cf: float, fixed_slots) -> dict:
+    """_moe_fixed_capacity (kappa/qwen3/ffn_moe.py:107-158) on the routing of reference_block."""
+    act = spec.act
+    x = inp["x"]
+    T, D = x.shape
+    E, K = spec.E, spec.K
+    M = T * K
+    idx, w = blk["idx"], blk["w"]
+    expert_flat = idx.reshape(M)
+    token_flat = np.repeat(np.arange(T, dtype=np.int32), K)
+    w_flat = w.reshape(M)
+    order = np.lexsort((token_flat, expert_flat))  # sort by expert, then token (:130)
+    sorted_e = expert_flat[order]
+    sorted_x = x[token_flat[order]]
+    # _slot_within_expert: 0, 1, ... along each run of equal experts (:59-71)
+    slot = np.zeros(M, np.int32)
+    for i in range(1, M):
+        slot[i] = slot[i - 1] + 1 if sorted_e[i] == sorted_e[i - 1] else 0
+    c_dyn, c_buf = fixed_capacity_slots(T, K, E, cf, fixed_slots)
+    valid = (slot < c_dyn) & (slot < c_buf)
+    buf = np.zeros((E, c_buf, D), np.float64)
+    safe_s = np.where(valid, slot, 0)
+    for i in range(M):
+        if valid[i]:
+            buf[sorted_e[i], safe_s[i]] += sorted_x[i]
+    wg = to_compute_dtype(inp["gate"], act).astype(np.float64)
+    wu = to_compute_dtype(inp["up"], act).astype(np.float64)
+    wd = to_compute_dtype(inp["down"], act).astype(np.float64)
+    g = as_act(np.einsum("ecd,edi->eci", buf, wg), act)
+    u = as_act(np.einsum("ecd,edi->eci", buf, wu), act)
+    h = as_act(silu64(g.astype(np.float64)) * u.astype(np.float64), act)
+    y_b = as_act(np.einsum("eci,eid->ecd", h.astype(np.float64), wd), act)
+    y_pick = np.where(valid[:, None], y_b[sorted_e, safe_s], 0.0)
+    inv = np.zeros(M, np.int32)
+    inv[order] = np.arange(M, dtype=np.int32)
+    y_assign = y_pick[inv]  # gather order (t, j)
+    out = as_act(np.sum((y_assign * w_flat[:, None].astype(np.float64)).reshape(T, K, D), axis=1), act)
+    # inv with -1 for dropped assignments (position in the stable order otherwise)
+    inv_cap = np.where(valid[inv], inv, -1).astype(np.int32)
+    return {
+        "idx": idx,
+        "w": w,
+        "capacity": np.int32(min(c_dyn, c_buf)),
+        "inv_cap": inv_cap,
+        "y_assign": y_assign.astype(np.float32).reshape(T, K, D),
+        "out": out.astype(np.float32),
+    }
+
+
 def main() -> None:
     meta = {}
     for spec in GOLDEN_SPECS:
@@ -125,6 +189,22 @@ def main() -> None:
         np.savez_compressed(os.path.join(HERE, f"{spec.name}.npz"), **ref)
         meta[spec.name] = {"spec": spec.as_dict(), "input_sha256": digest(inp), "min_gap": float(np.min(ref["gap"]))}
         print(f"{spec.name}: T={spec.T} D={spec.D} E={spec.E} K={spec.K} I={spec.I} min_gap={np.min(ref['gap']):.3e}")
+    for spec, cf, slots in CAPACITY_SPECS:
+        inp = make_inputs(spec)
+        blk = reference_block(spec, inp)
+        ref = reference_fixed_capacity(spec, inp, blk, cf, slots)
+        np.savez_compressed(os.path.join(HERE, f"{spec.name}.npz"), **ref)
+        dropped = int(np.sum(ref["inv_cap"] < 0))
+        meta[spec.name] = {
+            "spec": spec.as_dict(),
+            "input_sha256": digest(inp),
+            "min_gap": float(np.min(blk["gap"])),
+            "capacity_factor": cf,
+            "fixed_slots": slots,
+            "capacity": int(ref["capacity"]),
+            "dropped": dropped,
+        }
+        print(f"{spec.name}: capacity {int(ref['capacity'])}, {dropped} of {spec.T * spec.K} assignments dropped")
     with open(os.path.join(HERE, "golden.json"), "w") as f:
         json.dump(meta, f, indent=1, sort_keys=True)
 

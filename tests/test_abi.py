@@ -33,15 +33,15 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_status_strings():
     L = _lib.lib()
-    assert L.kmoe_abi_version() == 1
+    assert L.kmoe_abi_version() == 2
     assert b"gfx950" in L.kmoe_version()
     for s in range(6):
         assert L.kmoe_status_string(s)
     assert L.kmoe_status_string(99) == b"unknown status"
 
 
-def desc(T=4, D=128, E=8, K=2, I=64, act=_lib.DTYPE_BF16, thr=64):
-    return _lib.KmoeDesc(T, D, E, K, I, act, thr)
+def desc(T=4, D=128, E=8, K=2, I=64, act=_lib.DTYPE_BF16, thr=64, cap=0):
+    return _lib.KmoeDesc(T, D, E, K, I, act, thr, cap)
 
 
 def status_and_msg(st):
@@ -56,6 +56,7 @@ def status_and_msg(st):
         (dict(K=0), "top_k"),
         (dict(K=9), "top_k"),
         (dict(act=_lib.DTYPE_I8), "act_dtype"),
+        (dict(cap=-1), "expert_capacity"),
     ],
 )
 def test_workspace_bytes_rejects_bad_desc(kw, frag):

@@ -328,3 +328,68 @@ def test_prepack_layout(dev):
     for which in (0, 1):
         np.testing.assert_array_equal(s13[:, :, which], oracle.bf16_round(ss[which]).reshape(E, I // 16, 16))
     np.testing.assert_array_equal(p.s2.cpu().numpy().reshape(E, D), oracle.bf16_round(ss[2]).reshape(E, D))
+
+
+# --- fixed_capacity (token dropping, kappa/qwen3/ffn_moe.py:107-158) ----------
+
+from inputs import CAPACITY_SPECS  # noqa: E402
+
+
+@pytest.mark.parametrize("case", CAPACITY_SPECS, ids=[c[0].name for c in CAPACITY_SPECS])
+def test_fixed_capacity_golden(dev, case):
+    """moe_swiglu_ffn with moe_impl='fixed_capacity' against the oracle and the
+    golden restatement: the same slot limit, the same dropped assignments."""
+    import dataclasses
+
+    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+    from kappa_amd.qwen3.ffn_moe import _fixed_capacity
+
+    spec, cf, slots = case
+    inp = make_inputs(spec)
+    bf16 = spec.act == "bf16"
+    x, r, (g, u, d) = spec_to_dev(spec, inp, dev)
+    cfg = moe_layer_config(hidden=spec.D, experts=spec.E, top_k=spec.K, intermediate=spec.I,
+                           moe_impl="fixed_capacity", moe_capacity_factor=cf)  # fmt: skip
+    if slots is not None:
+        cfg = dataclasses.replace(cfg, moe_fixed_capacity_slots=slots)
+    cap = _fixed_capacity(cfg, spec.T)
+    gold = np.load(f"tests/golden/{spec.name}.npz")
+    assert cap == int(gold["capacity"]) == oracle.capacity_slots(spec.T, spec.K, spec.E, cf, slots)
+    ref = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K,
+                         act_bf16=bf16, capacity=cap)  # fmt: skip
+    # dispatch stage: inv carries -1 exactly for the dropped assignments
+    rt = moe_stages.route(x, r, num_experts=spec.E, k=spec.K)
+    dp = moe_stages.dispatch(rt["idx"], rt["hist"], num_experts=spec.E, capacity=cap)
+    np.testing.assert_array_equal(dp["inv"].cpu().numpy(), ref["inv"])
+    np.testing.assert_array_equal(dp["inv"].cpu().numpy(), gold["inv_cap"])
+    out = moe_swiglu_ffn(x.reshape(1, spec.T, spec.D), r, g, u, d, cfg=cfg).reshape(spec.T, spec.D)
+    check_out(out.float().cpu().numpy(), ref["out"], bf16)
+    check_out(out.float().cpu().numpy(), gold["out"], bf16, "vs golden")
+
+
+@pytest.mark.parametrize("T,cf", [(64, 1.0), (4096, 1.0), (4096, 0.5)])
+def test_30b_fixed_capacity(dev, l30, T, cf):
+    """30B-A3B W8 layer with token dropping at decode and prefill sizes (sampled
+    tokens against the oracle); every token's kept experts match the slot rule."""
+    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+    from kappa_amd.qwen3.ffn_moe import _fixed_capacity
+
+    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I,
+                           moe_impl="fixed_capacity", moe_capacity_factor=cf)  # fmt: skip
+    cap = _fixed_capacity(cfg, T)
+    x = make_x(T, l30.D, seed=700 + T)
+    r, d = _route_and_dispatch(x, l30.router, l30.E, l30.K)
+    xn, idx, w, od = _check_routing(x, l30.router, l30.E, l30.K, r, d)
+    inv_cap = oracle.drop_over_capacity(idx, od, cap)
+    dc = moe_stages.dispatch(r["idx"], r["hist"], num_experts=l30.E, capacity=cap)
+    np.testing.assert_array_equal(dc["inv"].cpu().numpy(), inv_cap)
+    assert np.any(inv_cap < 0)
+    out = moe_swiglu_ffn(x.reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
+    rng = np.random.default_rng(T)
+    toks = np.unique(np.concatenate([rng.choice(T, size=min(32, T), replace=False), [0, T - 1]]))
+    rows_t = np.repeat(toks, l30.K)
+    rows_e = idx[toks].reshape(-1)
+    _, yo = oracle_rows(oracle, xn, rows_t, rows_e, l30.host())
+    kept = inv_cap.reshape(T, l30.K)[toks].reshape(-1)
+    ref = oracle.combine(yo, np.where(kept >= 0, np.arange(len(rows_t)), -1).astype(np.int32), w[toks], True)
+    check_out(bf16_np(out.reshape(T, l30.D))[toks], ref, True, "out rows")

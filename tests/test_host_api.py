@@ -59,3 +59,26 @@ def test_presets_match_reference_values():
     assert c.moe_impl == "gather_einsum" and c.moe_ragged_decode_token_threshold == 64
     with pytest.raises(ValueError, match="unknown preset"):
         qwen3_config_for_preset("nope")
+
+
+def test_fixed_capacity_slots_follow_reference_formula():
+    """c_buf (kappa/qwen3/ffn_moe.py:23-31) and c_dyn (:136-139), including the
+    float32 round-half-even of c_dyn and the floor of one slot."""
+    from kappa_amd.qwen3.ffn_moe import _fixed_capacity, _fixed_capacity_buffer_slots
+
+    c30 = moe_layer_config(hidden=2048, experts=128, top_k=8, intermediate=768, moe_impl="fixed_capacity")
+    assert _fixed_capacity_buffer_slots(c30) == 640  # ceil(1.25 * 8192 * 8 / 128)
+    assert _fixed_capacity(c30, 4096) == 320  # 1.25 * 32768 / 128
+    assert _fixed_capacity(c30, 64) == 5
+    assert _fixed_capacity(c30, 1) == 1  # round(0.078125) = 0 -> floor of one slot
+    # c_dyn capped by the static buffer
+    assert _fixed_capacity(c30, 8192 * 4) == 640
+    # explicit slots override the derived buffer depth
+    c_fix = dataclasses.replace(c30, moe_fixed_capacity_slots=3)
+    assert _fixed_capacity_buffer_slots(c_fix) == 3 and _fixed_capacity(c_fix, 4096) == 3
+    # half-even: cf * T*K / E = 2.5 -> 2, 3.5 -> 4
+    c_he = moe_layer_config(hidden=16, experts=8, top_k=2, intermediate=32, moe_capacity_factor=1.25)
+    assert _fixed_capacity(c_he, 8) == 2  # 1.25 * 16 / 8 = 2.5
+    assert _fixed_capacity(c_he, 11) == 3  # 1.25 * 22 / 8 = 3.4375
+    c_he2 = dataclasses.replace(c_he, moe_capacity_factor=1.75)
+    assert _fixed_capacity(c_he2, 8) == 4  # 1.75 * 16 / 8 = 3.5

@@ -84,3 +84,35 @@ def test_tie_kats():
         best = int(np.argmax(lg[t, :4]))
         assert r["idx"][t, 0] == best and r["idx"][t, 1] == best + 4
         assert r["w"][t, 0] == r["w"][t, 1]
+
+
+from inputs import CAPACITY_SPECS  # noqa: E402
+
+
+@pytest.mark.parametrize("case", CAPACITY_SPECS, ids=[c[0].name for c in CAPACITY_SPECS])
+def test_oracle_fixed_capacity_matches_golden(case):
+    """fixed_capacity (kappa/qwen3/ffn_moe.py:107-158): the slot limit, which
+    assignments are dropped (exact), and the outputs of the kept ones."""
+    spec, cf, slots = case
+    inp = make_inputs(spec)
+    assert digest(inp) == META[spec.name]["input_sha256"], "input generator drifted from the golden vectors"
+    g = np.load(os.path.join(HERE, f"{spec.name}.npz"))
+    cap = oracle.capacity_slots(spec.T, spec.K, spec.E, cf, slots)
+    assert cap == int(g["capacity"])
+    bf16 = spec.act == "bf16"
+    r = oracle.forward(
+        inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=bf16, capacity=cap
+    )
+    np.testing.assert_array_equal(r["idx"], g["idx"])
+    np.testing.assert_array_equal(r["inv"], g["inv_cap"])
+    assert np.any(r["inv"] < 0), "the case must drop something"
+    kept = r["inv"].reshape(spec.T, spec.K) >= 0
+    y_g = np.where(kept[..., None], r["y_sorted"][np.maximum(r["inv"], 0)].reshape(spec.T, spec.K, -1), 0.0)
+    if bf16:
+        for a, b in ((y_g, g["y_assign"]), (r["out"], g["out"])):
+            diff = np.abs(a - b)
+            assert np.mean(diff > 0) < 2e-3
+            assert np.all(diff <= 2.0**-7 * np.abs(b) + 1e-6)
+    else:
+        scale = max(float(np.abs(g["out"]).max()), 1e-30)
+        assert np.max(np.abs(r["out"] - g["out"])) <= 1e-5 * scale

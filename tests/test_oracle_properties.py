@@ -264,3 +264,78 @@ def test_w8_relative_error_matches_reference_check():
         y0 = np.einsum("td,hdk->thk", x, w)
         y1 = np.einsum("td,hdk->thk", x, q.astype(np.float32) * s)
         assert np.linalg.norm(y0 - y1) / np.linalg.norm(y0) <= 0.02
+
+
+# --- fixed_capacity (kappa/qwen3/ffn_moe.py:107-158) ---------------------------
+
+
+def test_capacity_slots_closed_forms():
+    """c_dyn = max(1, round_half_even(f32(cf) * f32(T*K) / f32(E))) and
+    c_buf = ceil(cf * 8192 * K / E) or the explicit slot count (:23-31, 136-141)."""
+    assert oracle.capacity_slots(4096, 8, 128, 1.25) == 320
+    assert oracle.capacity_slots(64, 8, 128, 1.25) == 5
+    assert oracle.capacity_slots(1, 8, 128, 1.25) == 1  # 0.078125 rounds to 0: floor of one
+    assert oracle.capacity_slots(8, 2, 8, 1.25) == 2  # 2.5 -> 2 (half to even)
+    assert oracle.capacity_slots(8, 2, 8, 1.75) == 4  # 3.5 -> 4
+    assert oracle.capacity_slots(32768, 8, 128, 1.25) == 640  # c_dyn 2560 capped by c_buf 640
+    assert oracle.capacity_slots(4096, 8, 128, 1.25, fixed_slots=7) == 7
+
+
+def _slots_brute(idx):
+    """_slot_within_expert by its definition: for each (t, j), the number of
+    earlier tokens that also chose that expert (the stable (expert, token) order)."""
+    T, K = idx.shape
+    slot = np.zeros((T, K), np.int32)
+    for t in range(T):
+        for j in range(K):
+            slot[t, j] = int(np.sum(idx[:t] == idx[t, j]))
+    return slot
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_drop_over_capacity_matches_slot_definition(seed):
+    rng = np.random.default_rng(300 + seed)
+    T, K, E = 37, 3, 7
+    idx = np.stack([rng.choice(E, size=K, replace=False) for _ in range(T)]).astype(np.int32)
+    disp = oracle.dispatch(idx, E)
+    slot = _slots_brute(idx)
+    for cap in (1, 2, 5, 100):
+        inv = oracle.drop_over_capacity(idx, disp, cap).reshape(T, K)
+        np.testing.assert_array_equal(inv < 0, slot >= cap)
+        np.testing.assert_array_equal(inv[inv >= 0], disp["inv"].reshape(T, K)[inv >= 0])
+
+
+def _tiny_block(seed, act_bf16):
+    from inputs import Spec, make_inputs
+
+    spec = Spec("cap_tiny", T=20, D=64, E=6, K=2, I=32, base_seed=400 + seed,
+                act="bf16" if act_bf16 else "f32", weights="w8c" if act_bf16 else "f32",
+                router="bf16" if act_bf16 else "f32")  # fmt: skip
+    return spec, make_inputs(spec)
+
+
+@pytest.mark.parametrize("act_bf16", [True, False])
+def test_capacity_at_or_above_largest_group_is_dropless(act_bf16):
+    spec, inp = _tiny_block(0, act_bf16)
+    args = (inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"])
+    a = oracle.forward(*args, k=spec.K, act_bf16=act_bf16)
+    b = oracle.forward(*args, k=spec.K, act_bf16=act_bf16, capacity=int(a["group_sizes"].max()))
+    np.testing.assert_array_equal(a["out"], b["out"])
+    assert np.all(b["inv"] >= 0)
+
+
+def test_dropped_assignments_remove_exactly_their_term():
+    """out(capacity) = out(dropless) with each dropped assignment's weighted term
+    removed: recomputed here with the dropless rows and a zero weight."""
+    spec, inp = _tiny_block(1, False)
+    args = (inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"])
+    a = oracle.forward(*args, k=spec.K, act_bf16=False)
+    b = oracle.forward(*args, k=spec.K, act_bf16=False, capacity=2)
+    dropped = (b["inv"] < 0).reshape(spec.T, spec.K)
+    assert dropped.any()
+    w0 = np.where(dropped, np.float32(0.0), a["w"]).astype(np.float32)
+    ref = oracle.combine(a["y_sorted"], a["inv"], w0, False)
+    np.testing.assert_allclose(b["out"], ref, rtol=0, atol=1e-7)
+    # tokens with nothing dropped are bit-identical to the dropless output
+    keep_all = ~dropped.any(axis=1)
+    np.testing.assert_array_equal(b["out"][keep_all], a["out"][keep_all])
