@@ -2,6 +2,7 @@
 """Benchmark: the Qwen3-30B-A3B W8 MoE layer on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--tokens T] [--copies R] [--sweep]
+    python bench.py --copy-calibration MIB   # plain device copies of MIB MiB (counter calibration)
 
 A step is one call of the whole MoE block (router, top-k, dispatch, SwiGLU
 experts, combine) on T tokens, through the C ABI (kmoe_forward). Inputs and
@@ -10,7 +11,7 @@ the 256 MB Infinity Cache, steps rotate over R independent weight copies
 (R x 604 MB) and R activation batches.
 
 Prints ONE JSON line on stdout (logs go to stderr):
-  value        decode tokens/s at T (default 64) = T*K / elapsed
+  value        decode tokens/s at T (default 64) = T * steps / elapsed
   roofline     the dominant decode kernel (gate/up + SwiGLU), HBM-bound:
                algorithmic bytes per launch / mean launch time from HIP events
   prefill      the 4096-token prefill chunk: tokens/s and the MFMA roofline
@@ -107,50 +108,68 @@ def time_forward(bounds, xs, outs, steps, warmup):
 
 
 def time_gate_up(bounds, xs, steps, decode: bool):
-    """Stage-by-stage steps with HIP events around the gate/up kernel (the dominant one).
+    """Mean duration of the gate/up kernel (the dominant one) from HIP events on
+    its stream around `steps` back-to-back launches that rotate over the weight
+    copies (routing and dispatch for each copy are computed first, untimed).
 
-    Returns (mean gate/up ms, mean active experts U, mean rows M)."""
+    Returns (mean gate/up ms, mean active experts U)."""
     import torch
 
     from kappa_amd.qwen3 import moe_stages
 
-    ev = []
+    items = []
     actives = []
-    for i in range(steps):
-        b = bounds[i % len(bounds)]
+    for i, b in enumerate(bounds):
         lay = b.layer
         x = xs[i % len(xs)]
         r = moe_stages.route(x, lay.router, num_experts=lay.E, k=lay.K)
         dsp = moe_stages.dispatch(r["idx"], r["hist"], num_experts=lay.E)
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        h, y = _gate_up_only(b, x, dsp, decode)
-        e1.record()
-        ev.append((e0, e1))
+        h = torch.empty((x.shape[0] * lay.K, lay.I), dtype=torch.bfloat16, device=x.device)
+        items.append((b, x, dsp, h))
         actives.append(dsp["active"][lay.E : lay.E + 1])
+    for it in items:
+        _gate_up_only(*it, decode)
     torch.cuda.synchronize()
-    ms = [a.elapsed_time(c) for a, c in ev]
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        _gate_up_only(*items[i % len(items)], decode)
+    e1.record()
+    torch.cuda.synchronize()
     U = float(torch.cat(actives).float().mean().item())
-    return statistics.mean(ms[1:] if len(ms) > 2 else ms), U, ms
+    return e0.elapsed_time(e1) / steps, U
 
 
-def _gate_up_only(b, x, dsp, decode):
+def _gate_up_only(b, x, dsp, h, decode):
     import torch
 
     from kappa_amd import _lib
 
     lay = b.layer
     T = x.shape[0]
-    h = torch.empty((T * lay.K, lay.I), dtype=torch.bfloat16, device=x.device)
-    desc = type(b.desc)(T, lay.D, lay.E, lay.K, lay.I, 1, 64 if decode else 0)
+    desc = type(b.desc)(T, lay.D, lay.E, lay.K, lay.I, 1, 64 if decode else 0, 0)
     _lib.check(
         _lib.lib().kmoe_expert_gate_up(
             desc, x.data_ptr(), dsp["offsets"].data_ptr(), dsp["active"].data_ptr(), dsp["sorted_token"].data_ptr(),
             dsp["sorted_expert"].data_ptr(), b.g, b.u, b.p, h.data_ptr(), torch.cuda.current_stream().cuda_stream,
         )
     )  # fmt: skip
-    return h, None
+    return h
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` on `workload` from the rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE, copy-calibrated) committed under profiles/, or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_30b.md")
+    try:
+        for line in open(path):
+            f = line.split()
+            if len(f) >= 4 and f[0] == "traffic" and f[1] == kernel and f[2] == workload:
+                return int(f[3])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(layer, T, budget_s=12.0, max_reps=20):
@@ -208,6 +227,14 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="also time decode T in {1, 8, 32}")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument(
+        "--copy-calibration",
+        type=int,
+        default=0,
+        metavar="MIB",
+        help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that scales the "
+        "FETCH_SIZE / WRITE_SIZE counters) and exit",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -219,6 +246,16 @@ def main():
 
     sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
     import torch
+
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20)
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: 5 copies of {args.copy_calibration} MiB ({n} bytes read and written each)")
+        return
 
     from kappa_amd import _lib
 
@@ -243,7 +280,7 @@ def main():
     tok_s = T * args.steps / secs
     log(f"bench: decode T={T}: {ms_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s")
 
-    gu_ms, U, _ = time_gate_up(bounds, xs, max(args.steps, 16), decode=True)
+    gu_ms, U = time_gate_up(bounds, xs, max(args.steps, 16), decode=True)
     M = T * K
     gu_bytes = U * (2 * D * I + 2 * I * 4) + T * D * 2 + M * I * 2
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
@@ -279,7 +316,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": gu_gbs / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic("k_gateup_decode", f"decode_T{T}"),
             "algorithmic_bytes_per_launch": gu_bytes,
             "mean_launch_us": gu_ms * 1e3,
             "active_experts": U,
@@ -295,7 +332,7 @@ def main():
             xs_s = [x[:Ts].contiguous() for x in xs]
             o_s = [torch.empty(Ts, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
             s = time_forward(bs, xs_s, o_s, args.steps, args.warmup)
-            gms, Us, _ = time_gate_up(bs, xs_s, max(args.steps, 16), decode=True)
+            gms, Us = time_gate_up(bs, xs_s, max(args.steps, 16), decode=True)
             gb = Us * (2 * D * I + 2 * I * 4) + Ts * D * 2 + Ts * K * I * 2
             lb = Us * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 2 * (2 * Ts * D)
             sweep[str(Ts)] = {
@@ -319,7 +356,7 @@ def main():
         op = [torch.empty(Tp, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
         psteps = max(10, args.steps // 5)
         s = time_forward(bp, xp, op, psteps, 3)
-        gms, Up, _ = time_gate_up(bp, xp, psteps, decode=False)
+        gms, Up = time_gate_up(bp, xp, psteps, decode=False)
         Mp = Tp * K
         flops_gu = 2.0 * Mp * D * 2 * I
         flops_layer = 2.0 * Tp * K * 3 * D * I + 2.0 * Tp * D * E
@@ -331,13 +368,13 @@ def main():
             "layer_tflops": flops_layer / (s / psteps) / 1e12,
             "layer_mfma_frac": flops_layer / (s / psteps) / 1e12 / BF16_PEAK_TFLOPS,
             "roofline": {
-                "kernel": "k_prefill<true> (gate/up grouped GEMM + SwiGLU)",
+                "kernel": "k_gemm<true> (gate/up grouped GEMM + SwiGLU)",
                 "bound": "mfma",
                 "achieved": tf,
                 "peak": BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": tf / BF16_PEAK_TFLOPS,
-                "traffic": None,
+                "traffic": measured_traffic("k_gemm_gateup", f"prefill_T{Tp}"),
                 "algorithmic_flops_per_launch": flops_gu,
                 "mean_launch_us": gms * 1e3,
             },
