@@ -94,7 +94,7 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Workspace {
   size_t topk_idx, topk_w, hist, group_sizes, offsets, active, sorted_token, sorted_expert, inv, h_sorted,
-      y_sorted, total;
+      y_sorted, route_part, total;
 };
 
 Workspace layout(const kmoe_desc& d) {
@@ -121,6 +121,7 @@ Workspace layout(const kmoe_desc& d) {
   w.inv = take(4 * M);
   w.h_sorted = take(act * M * I);
   w.y_sorted = take(act * M * D);
+  w.route_part = take(T <= (size_t)kmoe::kDispatchBlock ? 4 * kmoe_host::route_split_part_floats(d) : 0);
   w.total = o;
   return w;
 }
@@ -339,10 +340,15 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
   int32_t* inv = reinterpret_cast<int32_t*>(base + w.inv);
   void* hs = base + w.h_sorted;
   void* ys = base + w.y_sorted;
-  // one 64-token chunk: the dispatch counts the chunk itself, no histogram pass
-  int32_t* h = desc->tokens > kmoe::kDispatchBlock ? hist : nullptr;
-  KMOE_HIP(kmoe_host::launch_route(*desc, x, *router, nullptr, tidx, tw, h, st), "route kernels");
-  KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, h, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
+  if (desc->tokens <= kmoe::kDispatchBlock) {
+    // one 64-token chunk: the split router; the dispatch counts the chunk itself
+    float* part = reinterpret_cast<float*>(base + w.route_part);
+    KMOE_HIP(kmoe_host::launch_route_split(*desc, x, *router, part, nullptr, tidx, tw, st), "route kernels");
+    KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, nullptr, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
+  } else {
+    KMOE_HIP(kmoe_host::launch_route(*desc, x, *router, nullptr, tidx, tw, hist, st), "route kernels");
+    KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, hist, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
+  }
   KMOE_TRY(expert_stage(*desc, kmoe_host::kStageGateUp | kmoe_host::kStageDown, x, off, act, stok, sexp, gate, up,
                         down, packed, hs, ys, st));
   KMOE_HIP(kmoe_host::launch_combine(*desc, ys, inv, tw, out, st), "combine kernel");

@@ -10,6 +10,11 @@ namespace kmoe_host {
 // route.hip
 hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* logits, int32_t* topk_idx,
                         float* topk_w, int32_t* hist, hipStream_t st);
+// Split router (many blocks per token; same logits and selections as
+// launch_route): part holds route_split_part_floats(d) floats of workspace.
+size_t route_split_part_floats(const kmoe_desc& d);
+hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part, float* logits,
+                              int32_t* topk_idx, float* topk_w, hipStream_t st);
 hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const int32_t* hist, int32_t* group_sizes,
                            int32_t* offsets, int32_t* active, int32_t* sorted_token, int32_t* sorted_expert,
                            int32_t* inv, hipStream_t st);

@@ -12,9 +12,9 @@
 namespace kmoe {
 
 // ---------------------------------------------------------------------------
-// Router weight rows. A lane owns EPL (8 or 16) consecutive experts of one
-// hidden row and loads them with one or two 16-byte loads (8 bytes for an
-// int8 router with EPL = 8); LPR = E / EPL lanes cover a row contiguously.
+// Router weight rows. A lane owns EPL consecutive experts of one hidden row
+// and loads them with 16-byte loads, or one 8- or 4-byte load when the EPL
+// experts take 8 or 4 bytes; LPR = E / EPL lanes cover a row contiguously.
 // ---------------------------------------------------------------------------
 template <int RT, int EPL>
 struct RouterRow {
@@ -24,16 +24,23 @@ struct RouterRow {
     uint32_t w[kWords];
   };
   __device__ __forceinline__ static void load(const void* rw, int64_t elem, Raw& r) {
-    const char* p = reinterpret_cast<const char*>(rw) + elem * (kBytes / EPL);
+    load_at(reinterpret_cast<const char*>(rw) + elem * (kBytes / EPL), 0, r);
+  }
+  // row pointer (uniform across the wave) plus a per-lane byte offset
+  __device__ __forceinline__ static void load_at(const char* row, int off, Raw& r) {
+    const char* p = row + off;
     if constexpr (kWords % 4 == 0) {
 #pragma unroll
       for (int q = 0; q < kWords / 4; ++q) {
         const uint4 v = reinterpret_cast<const uint4*>(p)[q];
         r.w[4 * q] = v.x, r.w[4 * q + 1] = v.y, r.w[4 * q + 2] = v.z, r.w[4 * q + 3] = v.w;
       }
-    } else {
+    } else if constexpr (kWords == 2) {
       const uint2 v = *reinterpret_cast<const uint2*>(p);
       r.w[0] = v.x, r.w[1] = v.y;
+    } else {
+      static_assert(kWords == 1, "router rows of 4, 8 or 16k bytes per lane");
+      r.w[0] = *reinterpret_cast<const uint32_t*>(p);
     }
   }
   // to_compute_dtype(router_w, f32) (kappa/qwen3/quant.py:34-38): int8 is f32(q) * f32(scale)
@@ -347,6 +354,152 @@ __global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int 
 }
 
 // ---------------------------------------------------------------------------
+// Split router for small token counts (decode): the same canonical logits as
+// k_route, computed by many blocks per token instead of one.
+//
+// k_route_slices, block (g, tb): wave w runs the fmaf chain of slice
+// s = 4g + w for the TB tokens tb*TB .. tb*TB+TB-1, a lane owning EPL
+// consecutive experts (all 64 rows of the slice in flight at once when they
+// fit in 64 registers). The block then applies tree levels st = 1 and 2 to its
+// four slices (the zero-padded tree's aligned group of four) and writes the
+// group partial part[t][g][e], g < Q = max(1, P / 4).
+// k_route_finish, one wave per token: tree levels st = 4, 8, ... over the Q
+// group partials (the levels st >= 4 of the same tree), then the top-k and
+// softmax of k_route.
+// ---------------------------------------------------------------------------
+template <typename A, int RT, int EPL, int TB>
+__global__ __launch_bounds__(256) void k_route_slices(int T, int D, int E, int P, int Q, const A* __restrict__ x,
+                                                       const void* __restrict__ rw, const void* __restrict__ rscale,
+                                                       int scale_bf16, int scale_pc, float* __restrict__ part) {
+  using Row = RouterRow<RT, EPL>;
+  constexpr int U = Row::kWords <= 1 ? 64 : 64 / Row::kWords;  // rows per load stage
+  __shared__ float xs[4][kRouterSlice][TB];
+  __shared__ float red[2][TB * EPL][64];
+  const int g = blockIdx.x, t0 = blockIdx.y * TB;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int s = 4 * g + w;
+  const int d0 = s * kRouterSlice;
+  for (int i = threadIdx.x; i < 4 * kRouterSlice * TB; i += blockDim.x) {
+    const int tt = i % TB, r = (i / TB) % kRouterSlice, ws = i / (TB * kRouterSlice);
+    const int d = (4 * g + ws) * kRouterSlice + r;
+    xs[ws][r][tt] = (t0 + tt < T && d < D) ? Act<A>::load(x, (int64_t)(t0 + tt) * D + d) : 0.0f;
+  }
+  const int LPR = (E + EPL - 1) / EPL;
+  const int e0 = lane * EPL;
+  float sc[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    sc[i] = 0.0f;
+    if (RT == 2 && e0 + i < E) sc[i] = load_scale(rscale, scale_bf16, scale_pc ? e0 + i : 0);
+  }
+  float acc[TB][EPL];
+#pragma unroll
+  for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) acc[tt][i] = 0.0f;
+  __syncthreads();
+  if (lane < LPR && d0 < D) {
+    const int n = min(kRouterSlice, D - d0);
+    if (E % EPL == 0 && n == kRouterSlice) {
+      // row pointers are uniform (scalar registers), the lane offset is e0
+      constexpr int kBpe = Row::kBytes / EPL;
+      const char* row0 = reinterpret_cast<const char*>(rw) + (int64_t)d0 * E * kBpe;
+      const int64_t pitch = (int64_t)E * kBpe;
+      const int loff = e0 * kBpe;
+      for (int db = 0; db < kRouterSlice; db += U) {
+        typename Row::Raw raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) Row::load_at(row0 + (db + u) * pitch, loff, raw[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float r[EPL];
+          Row::convert(raw[u], sc, r);
+#pragma unroll
+          for (int tt = 0; tt < TB; ++tt) {
+            const float xv = xs[w][db + u][tt];
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) acc[tt][i] = __builtin_fmaf(xv, r[i], acc[tt][i]);
+          }
+        }
+      }
+    } else {
+      for (int r0 = 0; r0 < n; ++r0) {
+        float r[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+          r[i] = (e0 + i < E) ? Row::load1(rw, (int64_t)(d0 + r0) * E + e0 + i, sc[i]) : 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < TB; ++tt) {
+          const float xv = xs[w][r0][tt];
+#pragma unroll
+          for (int i = 0; i < EPL; ++i) acc[tt][i] = __builtin_fmaf(xv, r[i], acc[tt][i]);
+        }
+      }
+    }
+  }
+  // tree levels st = 1 (slices 0+1, 2+3) and st = 2 (0+2) of the group
+  if (w & 1) {
+#pragma unroll
+    for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) red[w >> 1][tt * EPL + i][lane] = acc[tt][i];
+  }
+  __syncthreads();
+  if (!(w & 1) && 1 < P) {
+#pragma unroll
+    for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) acc[tt][i] = acc[tt][i] + red[w >> 1][tt * EPL + i][lane];
+  }
+  __syncthreads();
+  if (w == 2) {
+#pragma unroll
+    for (int tt = 0; tt < TB; ++tt)
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) red[0][tt * EPL + i][lane] = acc[tt][i];
+  }
+  __syncthreads();
+  if (w != 0 || lane >= LPR) return;
+#pragma unroll
+  for (int tt = 0; tt < TB; ++tt) {
+    if (t0 + tt >= T) break;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const float v = 2 < P ? acc[tt][i] + red[0][tt * EPL + i][lane] : acc[tt][i];
+      if (e0 + i < E) part[((int64_t)(t0 + tt) * Q + g) * E + e0 + i] = v;
+    }
+  }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route_finish(int T, int E, int K, int Q, const float* __restrict__ part,
+                                                       float* __restrict__ logits, int32_t* __restrict__ topk_idx,
+                                                       float* __restrict__ topk_w, int out_bf16) {
+  __shared__ TopkLds tk[4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + w;
+  if (t >= T) return;  // per wave: this kernel has no block-wide barrier
+  float v[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    float p[kMaxRouterSlices / 4];
+#pragma unroll
+    for (int q = 0; q < kMaxRouterSlices / 4; ++q)
+      p[q] = (q < Q && e < E) ? part[((int64_t)t * Q + q) * E + e] : 0.0f;
+#pragma unroll
+    for (int st = 1; st < kMaxRouterSlices / 4; st <<= 1)
+      if (st < Q)
+#pragma unroll
+        for (int q = 0; q + st < kMaxRouterSlices / 4; q += 2 * st) p[q] = p[q] + p[q + st];
+    const float l = p[0];
+    v[i] = (e < E && l == l) ? l : -INFINITY;
+    if (logits && e < E) logits[(int64_t)t * E + e] = l;
+  }
+  wave_topk<EPL>(t, E, K, v, topk_idx, topk_w, out_bf16, nullptr, tk[w]);
+}
+
+// ---------------------------------------------------------------------------
 // Dispatch: stable counting sort of the row-major (t, j) assignments by expert
 // (jnp.argsort(stable=True) over the flattened top-k indices).
 //
@@ -644,6 +797,107 @@ hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& r,
   const int T = (int)d.tokens, E = (int)d.num_experts, K = (int)d.top_k;
   const int nblk = (T + kDispatchBlock - 1) / kDispatchBlock;
   hipLaunchKernelGGL(k_dispatch_count, dim3(nblk), dim3(256), 0, st, T, E, K, topk_idx, hist);
+  return hipGetLastError();
+}
+
+// Split router: experts per lane for the slice kernel (>= 4 bytes of weights
+// per row and lane, at most 64 lanes per row), tokens per block, group count.
+struct SplitShape {
+  int EPL, TB, P, Q;
+};
+
+static SplitShape split_shape(const kmoe_desc& d, const kmoe_weight& r) {
+  SplitShape sh;
+  const int E = (int)d.num_experts, T = (int)d.tokens;
+  const int S = (int)((d.hidden + kRouterSlice - 1) / kRouterSlice);
+  const int min_epl = r.dtype == KMOE_DTYPE_F32 ? 1 : (r.dtype == KMOE_DTYPE_BF16 ? 2 : 4);
+  sh.EPL = min_epl;
+  while (sh.EPL * 64 < E) sh.EPL <<= 1;
+  sh.TB = T <= 16 ? 1 : (T <= 64 ? 2 : 4);
+  sh.P = 1;
+  while (sh.P < S) sh.P <<= 1;
+  sh.Q = sh.P >= 4 ? sh.P / 4 : 1;
+  return sh;
+}
+
+size_t route_split_part_floats(const kmoe_desc& d) {
+  const int S = (int)((d.hidden + kRouterSlice - 1) / kRouterSlice);
+  int P = 1;
+  while (P < S) P <<= 1;
+  const int Q = P >= 4 ? P / 4 : 1;
+  return (size_t)d.tokens * Q * d.num_experts;
+}
+
+template <typename A, int RT, int EPL, int TB>
+static void launch_slices(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part, hipStream_t st) {
+  const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts;
+  const int scale_bf16 = (r.dtype == KMOE_DTYPE_I8 && r.scale_dtype == KMOE_DTYPE_BF16) ? 1 : 0;
+  const int scale_pc = (r.dtype == KMOE_DTYPE_I8 && r.scale_kind == KMOE_SCALE_CHANNEL) ? 1 : 0;
+  hipLaunchKernelGGL((k_route_slices<A, RT, EPL, TB>), dim3(sh.Q, (T + TB - 1) / TB), dim3(256), 0, st, T, D, E,
+                     sh.P, sh.Q, reinterpret_cast<const A*>(x), r.values, r.scale, scale_bf16, scale_pc, part);
+}
+
+template <typename A, int RT, int EPL>
+static void slices_tb(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part, hipStream_t st) {
+  if (sh.TB == 1) return launch_slices<A, RT, EPL, 1>(d, sh, x, r, part, st);
+  if (sh.TB == 2) return launch_slices<A, RT, EPL, 2>(d, sh, x, r, part, st);
+  return launch_slices<A, RT, EPL, 4>(d, sh, x, r, part, st);
+}
+
+template <typename A, int RT>
+static void slices_epl(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part, hipStream_t st) {
+  switch (sh.EPL) {
+    case 1:
+      if constexpr (RT == 0) return slices_tb<A, RT, 1>(d, sh, x, r, part, st);
+      [[fallthrough]];
+    case 2:
+      if constexpr (RT != 2) return slices_tb<A, RT, 2>(d, sh, x, r, part, st);
+      [[fallthrough]];
+    case 4:
+      return slices_tb<A, RT, 4>(d, sh, x, r, part, st);
+    case 8:
+      return slices_tb<A, RT, 8>(d, sh, x, r, part, st);
+    default:
+      return slices_tb<A, RT, 16>(d, sh, x, r, part, st);
+  }
+}
+
+template <typename A>
+static void slices_rt(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part, hipStream_t st) {
+  if (r.dtype == KMOE_DTYPE_F32) return slices_epl<A, 0>(d, sh, x, r, part, st);
+  if (r.dtype == KMOE_DTYPE_BF16) return slices_epl<A, 1>(d, sh, x, r, part, st);
+  return slices_epl<A, 2>(d, sh, x, r, part, st);
+}
+
+template <int EPL>
+static void launch_finish(const kmoe_desc& d, const SplitShape& sh, const float* part, float* logits,
+                          int32_t* topk_idx, float* topk_w, hipStream_t st) {
+  const int T = (int)d.tokens, E = (int)d.num_experts, K = (int)d.top_k;
+  const int out_bf16 = d.act_dtype == KMOE_DTYPE_BF16 ? 1 : 0;
+  hipLaunchKernelGGL((k_route_finish<EPL>), dim3((T + 3) / 4), dim3(256), 0, st, T, E, K, sh.Q, part, logits,
+                     topk_idx, topk_w, out_bf16);
+}
+
+hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& r, float* part, float* logits,
+                              int32_t* topk_idx, float* topk_w, hipStream_t st) {
+  const SplitShape sh = split_shape(d, r);
+  if (d.act_dtype == KMOE_DTYPE_BF16)
+    slices_rt<uint16_t>(d, sh, x, r, part, st);
+  else
+    slices_rt<float>(d, sh, x, r, part, st);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int E = (int)d.num_experts;
+  if (E <= 64)
+    launch_finish<1>(d, sh, part, logits, topk_idx, topk_w, st);
+  else if (E <= 128)
+    launch_finish<2>(d, sh, part, logits, topk_idx, topk_w, st);
+  else if (E <= 256)
+    launch_finish<4>(d, sh, part, logits, topk_idx, topk_w, st);
+  else if (E <= 512)
+    launch_finish<8>(d, sh, part, logits, topk_idx, topk_w, st);
+  else
+    launch_finish<16>(d, sh, part, logits, topk_idx, topk_w, st);
   return hipGetLastError();
 }
 

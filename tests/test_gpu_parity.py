@@ -230,6 +230,32 @@ def test_decode_and_prefill_kernels_agree_at_threshold(dev, l30):
         check_out(outs[0], outs[1], True, f"T={T}")
 
 
+@pytest.mark.parametrize("T", [1, 2, 8, 16, 17, 40, 64])
+def test_whole_block_matches_staged_path(dev, l30, T):
+    """At T <= 64 the whole-block call routes with the split router (many blocks
+    per token); the staged calls use the one-block-per-token router. Both follow
+    the canonical summation order, so selections, weights and outputs are
+    bit-identical. The skewed router puts up to 64 rows on an expert."""
+    from kappa_amd.qwen3 import moe_stages
+    from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _moe_forward
+
+    for router in (l30.router, skew_router(l30.router, lam=1.5)):
+        x = make_x(T, l30.D, seed=700 + T)
+        x[:, 0] = 1.0
+        r, d = _route_and_dispatch(x, router, l30.E, l30.K)
+        h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K)
+        staged = moe_stages.combine(y, d["inv"], r["w"], k=l30.K)
+        packed = PACK_CACHE.get(l30.gate, l30.up, l30.down)
+        for _ in range(2):
+            out, idx, w = _moe_forward(
+                x.reshape(1, T, l30.D), router, l30.gate, l30.up, l30.down, num_experts=l30.E,
+                num_experts_per_tok=l30.K, decode_threshold=64, packed=packed, return_routing=True,
+            )  # fmt: skip
+            assert torch.equal(idx, r["idx"])
+            assert torch.equal(w.float(), r["w"])
+            assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
+
+
 def test_layout_native_experts_match_packed(dev, l30):
     from kappa_amd.qwen3 import moe_stages
 
