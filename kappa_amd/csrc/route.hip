@@ -720,13 +720,13 @@ static RouteShape route_shape(const kmoe_desc& d) {
   const int NG = r.P > r.SPW ? r.P / r.SPW : 1;
   r.G = NG > 16 ? NG / 16 : 1;
   r.NWB = NG / r.G;
-  // tokens per block: accumulators within the register budget, x stage and
-  // partials <= 64 KB, and enough blocks to cover the chip
+  // tokens per block: accumulators within the register budget, x stage <= 80 KB
+  // (two blocks per CU), partials <= 64 KB, and enough blocks to cover the chip
   int tb = 8;
   const int acc_cap = r.G > 1 ? 2 * r.EPL : 64;
   auto x_bytes = [&](int t) { return (size_t)4 * r.S * (kRouterSlice * t + 4); };
   auto part_bytes = [&](int t) { return (size_t)4 * r.NWB * t * E + r.NWB * sizeof(TopkLds); };
-  while (tb > 1 && (tb * r.EPL > acc_cap || x_bytes(tb) > 65536 || part_bytes(tb) > 65536)) tb >>= 1;
+  while (tb > 1 && (tb * r.EPL > acc_cap || x_bytes(tb) > 81920 || part_bytes(tb) > 65536)) tb >>= 1;
   while (tb > 1 && (T + tb - 1) / tb < 256) tb >>= 1;
   r.TB = tb;
   r.lds = std::max(x_bytes(tb), part_bytes(tb));
