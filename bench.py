@@ -107,6 +107,54 @@ def time_forward(bounds, xs, outs, steps, warmup):
     return t0.elapsed_time(t1) / 1e3
 
 
+def time_block(bounds, hs, outs, scale, steps, warmup, fused: bool):
+    """The MoE half of the layer, h + block(rms_norm(h)) (kappa/qwen3/block.py:196-207):
+    fused = one kmoe_forward_block call; otherwise kmoe_rms_norm, kmoe_forward and a
+    separate add, as the three steps run unfused. Returns seconds for `steps` steps."""
+    import torch
+
+    from kappa_amd import _lib
+
+    L = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    R = len(bounds)
+    h2 = torch.empty_like(hs[0])
+    moe = torch.empty_like(hs[0])
+
+    def step(i):
+        b = bounds[i % R]
+        h = hs[i % len(hs)]
+        out = outs[i % len(outs)]
+        if fused:
+            st = L.kmoe_forward_block(
+                b.desc, h.data_ptr(), scale.data_ptr(), _lib.DTYPE_BF16, 1e-6, b.r, b.g, b.u, b.d, b.p,
+                out.data_ptr(), None, None, b.ws.data_ptr(), b.ws.numel(), stream,
+            )  # fmt: skip
+            if st:
+                _lib.check(st)
+            return
+        _lib.check(L.kmoe_rms_norm(b.desc, h.data_ptr(), scale.data_ptr(), _lib.DTYPE_BF16, 1e-6, h2.data_ptr(), stream))
+        st = L.kmoe_forward(
+            b.desc, h2.data_ptr(), b.r, b.g, b.u, b.d, b.p, moe.data_ptr(), None, None, b.ws.data_ptr(), b.ws.numel(),
+            stream,
+        )  # fmt: skip
+        if st:
+            _lib.check(st)
+        torch.add(h, moe, out=out)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        step(warmup + i)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / 1e3
+
+
 def time_gate_up(bounds, xs, steps, decode: bool):
     """Mean duration of the gate/up kernel (the dominant one) from HIP events on
     its stream around `steps` back-to-back launches that rotate over the weight
@@ -324,6 +372,18 @@ def main():
         "layer_hbm_gbs": layer_bytes / (ms_step * 1e-3) / 1e9,
     }
     result["layer_hbm_frac"] = result["layer_hbm_gbs"] / HBM_PEAK_GBS
+
+    # the steps either side of the block: rms_norm in, residual add out
+    scale = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
+    fused_s = time_block(bounds, xs, outs, scale, args.steps, args.warmup, fused=True)
+    sep_s = time_block(bounds, xs, outs, scale, args.steps, args.warmup, fused=False)
+    result["block"] = {
+        "workload": f"h + moe_layer(rms_norm(h)), decode T={T}",
+        "fused_us_per_step": fused_s * 1e6 / args.steps,
+        "separate_us_per_step": sep_s * 1e6 / args.steps,
+        "moe_only_us_per_step": ms_step * 1e3,
+    }
+    log(f"bench: block {result['block']}")
 
     if args.sweep:
         sweep = {}

@@ -134,6 +134,28 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
                          int32_t* topk_idx_out, void* topk_w_out, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* The MoE half of a Qwen3 MoE layer with the steps on either side of the
+ * block fused in (kappa/qwen3/block.py:71-82, 153-164, 196-207):
+ *   h2  = rms_norm(h, norm_scale, epsilon)        (kappa/qwen3/norms.py:10-16)
+ *   out = h + moe_swiglu_ffn(h2, ...)             (rounded to h.dtype)
+ * h and out are [T,D] in the activation dtype (out must not alias h);
+ * norm_scale [D] is F32 or BF16 (pre_ffn_norm). h2 lives in the workspace
+ * (kmoe_workspace_bytes covers it); the residual add happens in the combine
+ * kernel, so the layer's separate add and its [T,D] round trip disappear.
+ * topk_idx_out / topk_w_out as for kmoe_forward. */
+kmoe_status kmoe_forward_block(const kmoe_desc* desc, const void* h, const void* norm_scale, kmoe_dtype norm_dtype,
+                               float epsilon, const kmoe_weight* router, const kmoe_weight* gate,
+                               const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed,
+                               void* out, int32_t* topk_idx_out, void* topk_w_out, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/* rms_norm (kappa/qwen3/norms.py:10-16) of x [T,D] into out [T,D] (activation
+ * dtype): the squares summed in the router's canonical slice order,
+ * r = 1 / sqrt(S / D + epsilon), out = round((x * r) * scale). The first step
+ * of kmoe_forward_block, for per-stage parity. */
+kmoe_status kmoe_rms_norm(const kmoe_desc* desc, const void* x, const void* scale, kmoe_dtype scale_dtype,
+                          float epsilon, void* out, void* stream);
+
 /* --- stages (per-stage parity; kmoe_forward chains exactly these) ------- */
 /* _route (kappa/qwen3/ffn_moe.py:38-56): logits [T,E] f32 (optional, may be
  * NULL), topk_idx [T,K] int32, topk_w [T,K] f32 holding values already

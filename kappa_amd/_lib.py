@@ -41,6 +41,8 @@ EXPORTS = (
     "kmoe_workspace_bytes",
     "kmoe_prepack_bytes",
     "kmoe_forward",
+    "kmoe_forward_block",
+    "kmoe_rms_norm",
     "kmoe_route",
     "kmoe_dispatch",
     "kmoe_expert_ffn",
@@ -118,6 +120,12 @@ def _declare(L: ctypes.CDLL) -> None:
     L.kmoe_forward.restype = ctypes.c_int
     L.kmoe_forward.argtypes = [_DP, _P, _WP, _WP, _WP, _WP, _PP, _P, _P, _P, _P, ctypes.c_size_t, _P]
     L.kmoe_route.restype = ctypes.c_int
+    L.kmoe_forward_block.restype = ctypes.c_int
+    L.kmoe_forward_block.argtypes = [
+        _DP, _P, _P, ctypes.c_int, ctypes.c_float, _WP, _WP, _WP, _WP, _PP, _P, _P, _P, _P, ctypes.c_size_t, _P,
+    ]  # fmt: skip
+    L.kmoe_rms_norm.restype = ctypes.c_int
+    L.kmoe_rms_norm.argtypes = [_DP, _P, _P, ctypes.c_int, ctypes.c_float, _P, _P]
     L.kmoe_route.argtypes = [_DP, _P, _WP, _P, _P, _P, _P, _P, _P]
     L.kmoe_dispatch.restype = ctypes.c_int
     L.kmoe_dispatch.argtypes = [_DP, _P, _P, _P, _P, _P, _P, _P, _P, _P]

@@ -20,7 +20,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkmoe.so")
-SOURCES = ["api.hip", "route.hip", "expert.hip", "weights.hip"]
+SOURCES = ["api.hip", "route.hip", "expert.hip", "weights.hip", "block.hip"]
 ARCH = os.environ.get("KMOE_OFFLOAD_ARCH", "gfx950")
 
 
@@ -39,6 +39,7 @@ def compile_flags() -> list[str]:
         "-fPIC",
         "-Wall",
         "-Wno-unused-command-line-argument",
+        "-fhip-fp32-correctly-rounded-divide-sqrt",
         "-Xclang",
         "-target-feature",
         "-Xclang",

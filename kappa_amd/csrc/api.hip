@@ -94,7 +94,7 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Workspace {
   size_t topk_idx, topk_w, hist, group_sizes, offsets, active, sorted_token, sorted_expert, inv, h_sorted,
-      y_sorted, route_part, total;
+      y_sorted, route_part, normed, total;
 };
 
 Workspace layout(const kmoe_desc& d) {
@@ -122,6 +122,7 @@ Workspace layout(const kmoe_desc& d) {
   w.h_sorted = take(act * M * I);
   w.y_sorted = take(act * M * D);
   w.route_part = take(T <= (size_t)kmoe::kDispatchBlock ? 4 * kmoe_host::route_split_part_floats(d) : 0);
+  w.normed = take(act * T * D);  // rms_norm(h) for kmoe_forward_block
   w.total = o;
   return w;
 }
@@ -308,10 +309,12 @@ kmoe_status kmoe_combine(const kmoe_desc* desc, const void* y_sorted, const int3
   return KMOE_OK;
 }
 
-kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight* router, const kmoe_weight* gate,
-                         const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed, void* out,
-                         int32_t* topk_idx_out, void* topk_w_out, void* workspace, size_t workspace_bytes,
-                         void* stream) {
+}  // extern "C"
+
+namespace {
+
+kmoe_status check_forward_args(const kmoe_desc* desc, const kmoe_weight* router, const kmoe_weight* gate,
+                               const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed) {
   KMOE_TRY(check_desc(desc));
   KMOE_TRY(check_weight(router, "router"));
   KMOE_TRY(check_packed_arg(*desc, packed));
@@ -320,15 +323,19 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
     KMOE_TRY(check_weight(up, "up"));
     KMOE_TRY(check_weight(down, "down"));
   }
-  if (desc->tokens > 0 && (!x || !out)) return fail(KMOE_ERR_INVALID_ARG, "kmoe_forward: x and out must be non-NULL");
-  const Workspace w = layout(*desc);
-  if (desc->tokens > 0 && (!workspace || workspace_bytes < w.total))
-    return fail(KMOE_ERR_WORKSPACE_TOO_SMALL, "workspace of %zu bytes is smaller than the %zu required",
-                workspace_bytes, w.total);
-  KMOE_TRY(device_status());
-  if (desc->tokens == 0) return KMOE_OK;
-  hipStream_t st = (hipStream_t)stream;
-  char* base = reinterpret_cast<char*>(workspace);
+  return KMOE_OK;
+}
+
+// The stage sequence of moe_swiglu_ffn on x. With a norm, x is the residual
+// stream h: the block runs on h2 = rms_norm(h) (norm->h2, computed by the
+// split router at T <= 64, else by the norm kernel) and the combine adds the
+// block's rounded output to h.
+kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host::SliceNorm* norm,
+                           const kmoe_weight* router, const kmoe_weight* gate, const kmoe_weight* up,
+                           const kmoe_weight* down, const kmoe_packed_experts* packed, void* out,
+                           int32_t* topk_idx_out, void* topk_w_out, char* base, const Workspace& w, hipStream_t st) {
+  const void* res = norm ? x : nullptr;
+  const void* xin = norm ? norm->h2 : x;  // the block's input, after the norm
   int32_t* tidx = reinterpret_cast<int32_t*>(base + w.topk_idx);
   float* tw = reinterpret_cast<float*>(base + w.topk_w);
   int32_t* hist = reinterpret_cast<int32_t*>(base + w.hist);
@@ -341,23 +348,90 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
   void* hs = base + w.h_sorted;
   void* ys = base + w.y_sorted;
   if (desc->tokens <= kmoe::kDispatchBlock) {
-    // one 64-token chunk: the split router; the dispatch counts the chunk itself
+    // one 64-token chunk: the split router (normalising its input rows when
+    // there is a norm); the dispatch counts the chunk itself
     float* part = reinterpret_cast<float*>(base + w.route_part);
-    KMOE_HIP(kmoe_host::launch_route_split(*desc, x, *router, part, nullptr, tidx, tw, st), "route kernels");
+    KMOE_HIP(kmoe_host::launch_route_split(*desc, x, *router, part, nullptr, tidx, tw, st, norm), "route kernels");
     KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, nullptr, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
   } else {
-    KMOE_HIP(kmoe_host::launch_route(*desc, x, *router, nullptr, tidx, tw, hist, st), "route kernels");
+    if (norm)
+      KMOE_HIP(kmoe_host::launch_rms_norm(*desc, x, norm->scale, norm->scale_bf16 ? KMOE_DTYPE_BF16 : KMOE_DTYPE_F32,
+                                          norm->eps, norm->h2, st),
+               "rms_norm kernel");
+    KMOE_HIP(kmoe_host::launch_route(*desc, xin, *router, nullptr, tidx, tw, hist, st), "route kernels");
     KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, hist, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
   }
-  KMOE_TRY(expert_stage(*desc, kmoe_host::kStageGateUp | kmoe_host::kStageDown, x, off, act, stok, sexp, gate, up,
+  KMOE_TRY(expert_stage(*desc, kmoe_host::kStageGateUp | kmoe_host::kStageDown, xin, off, act, stok, sexp, gate, up,
                         down, packed, hs, ys, st));
-  KMOE_HIP(kmoe_host::launch_combine(*desc, ys, inv, tw, out, st), "combine kernel");
+  KMOE_HIP(kmoe_host::launch_combine(*desc, ys, inv, tw, out, st, res), "combine kernel");
   if (topk_idx_out)
     KMOE_HIP(hipMemcpyAsync(topk_idx_out, tidx, sizeof(int32_t) * desc->tokens * desc->top_k,
                             hipMemcpyDeviceToDevice, st),
              "copy topk_idx");
   if (topk_w_out) KMOE_HIP(kmoe_host::launch_topk_w_cast(*desc, tw, topk_w_out, st), "topk_w cast");
   return KMOE_OK;
+}
+
+kmoe_status check_norm_args(const void* scale, kmoe_dtype scale_dtype, float epsilon) {
+  if (!scale) return fail(KMOE_ERR_INVALID_ARG, "norm scale pointer is NULL");
+  if (!is_float(scale_dtype)) return fail(KMOE_ERR_INVALID_ARG, "norm scale dtype must be F32 or BF16");
+  if (!(epsilon >= 0.0f) || epsilon > 1.0f)
+    return fail(KMOE_ERR_INVALID_ARG, "epsilon must be in [0, 1] (got %g)", (double)epsilon);
+  return KMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight* router, const kmoe_weight* gate,
+                         const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed, void* out,
+                         int32_t* topk_idx_out, void* topk_w_out, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  KMOE_TRY(check_forward_args(desc, router, gate, up, down, packed));
+  if (desc->tokens > 0 && (!x || !out)) return fail(KMOE_ERR_INVALID_ARG, "kmoe_forward: x and out must be non-NULL");
+  const Workspace w = layout(*desc);
+  if (desc->tokens > 0 && (!workspace || workspace_bytes < w.total))
+    return fail(KMOE_ERR_WORKSPACE_TOO_SMALL, "workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, w.total);
+  KMOE_TRY(device_status());
+  if (desc->tokens == 0) return KMOE_OK;
+  return forward_stages(desc, x, nullptr, router, gate, up, down, packed, out, topk_idx_out, topk_w_out,
+                        reinterpret_cast<char*>(workspace), w, (hipStream_t)stream);
+}
+
+kmoe_status kmoe_rms_norm(const kmoe_desc* desc, const void* x, const void* scale, kmoe_dtype scale_dtype,
+                          float epsilon, void* out, void* stream) {
+  KMOE_TRY(check_desc(desc));
+  KMOE_TRY(check_norm_args(scale, scale_dtype, epsilon));
+  if (desc->tokens > 0 && (!x || !out)) return fail(KMOE_ERR_INVALID_ARG, "kmoe_rms_norm: x and out must be non-NULL");
+  KMOE_TRY(device_status());
+  if (desc->tokens == 0) return KMOE_OK;
+  KMOE_HIP(kmoe_host::launch_rms_norm(*desc, x, scale, scale_dtype, epsilon, out, (hipStream_t)stream),
+           "rms_norm kernel");
+  return KMOE_OK;
+}
+
+kmoe_status kmoe_forward_block(const kmoe_desc* desc, const void* h, const void* norm_scale, kmoe_dtype norm_dtype,
+                               float epsilon, const kmoe_weight* router, const kmoe_weight* gate,
+                               const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed,
+                               void* out, int32_t* topk_idx_out, void* topk_w_out, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  KMOE_TRY(check_forward_args(desc, router, gate, up, down, packed));
+  KMOE_TRY(check_norm_args(norm_scale, norm_dtype, epsilon));
+  if (desc->tokens > 0 && (!h || !out))
+    return fail(KMOE_ERR_INVALID_ARG, "kmoe_forward_block: h and out must be non-NULL");
+  if (desc->tokens > 0 && out == h) return fail(KMOE_ERR_INVALID_ARG, "kmoe_forward_block: out must not alias h");
+  const Workspace w = layout(*desc);
+  if (desc->tokens > 0 && (!workspace || workspace_bytes < w.total))
+    return fail(KMOE_ERR_WORKSPACE_TOO_SMALL, "workspace of %zu bytes is smaller than the %zu required",
+                workspace_bytes, w.total);
+  KMOE_TRY(device_status());
+  if (desc->tokens == 0) return KMOE_OK;
+  char* base = reinterpret_cast<char*>(workspace);
+  const kmoe_host::SliceNorm nm{norm_scale, norm_dtype == KMOE_DTYPE_BF16 ? 1 : 0, epsilon, base + w.normed};
+  return forward_stages(desc, h, &nm, router, gate, up, down, packed, out, topk_idx_out, topk_w_out, base, w,
+                        (hipStream_t)stream);
 }
 
 kmoe_status kmoe_prepack(const kmoe_desc* desc, const kmoe_weight* gate, const kmoe_weight* up,

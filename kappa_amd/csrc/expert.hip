@@ -809,7 +809,9 @@ __global__ __launch_bounds__(256) void k_down_generic(int D, int I, const A* __r
 // sequential fmaf over j from +0.0f; no atomics, one writer per element.
 // A thread owns 8 consecutive columns (one 16-byte bf16 load per row); the
 // row indices and weights of a token are read first and the K row loads are
-// issued in batches of 8 before the FMAs.
+// issued in batches of 8 before the FMAs. With res (the residual stream h of
+// kappa/qwen3/block.py:207) the rounded sum is added to res[t, n] in f32 and
+// rounded again.
 // ---------------------------------------------------------------------------
 template <typename A>
 struct Vec8;
@@ -847,7 +849,7 @@ struct Vec8<float> {
 template <typename A>
 __global__ __launch_bounds__(256) void k_combine8(int T, int K, int D, const A* __restrict__ y,
                                                    const int32_t* __restrict__ inv, const float* __restrict__ w,
-                                                   A* __restrict__ out) {
+                                                   A* __restrict__ out, const A* __restrict__ res) {
   const int t = blockIdx.y;
   const int n0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (n0 >= D) return;
@@ -874,6 +876,13 @@ __global__ __launch_bounds__(256) void k_combine8(int T, int K, int D, const A* 
 #pragma unroll
         for (int v = 0; v < 8; ++v) acc[v] = __builtin_fmaf(wj[j], yv[j][v], acc[v]);
   }
+  if (res) {
+    // the block's output is rounded to the activation dtype, then added to h
+    float r[8];
+    Vec8<A>::load(res + (int64_t)t * D + n0, r);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) acc[v] = r[v] + Act<A>::round(acc[v]);
+  }
   Vec8<A>::store(out + (int64_t)t * D + n0, acc);
 }
 
@@ -881,7 +890,7 @@ __global__ __launch_bounds__(256) void k_combine8(int T, int K, int D, const A* 
 template <typename A>
 __global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* __restrict__ y,
                                                    const int32_t* __restrict__ inv, const float* __restrict__ w,
-                                                   A* __restrict__ out) {
+                                                   A* __restrict__ out, const A* __restrict__ res) {
   const int t = blockIdx.y;
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= D) return;
@@ -890,6 +899,7 @@ __global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* 
     const int p = inv[(int64_t)t * K + j];
     if (p >= 0) acc = __builtin_fmaf(w[(int64_t)t * K + j], Act<A>::load(y, (int64_t)p * D + n), acc);
   }
+  if (res) acc = Act<A>::load(res, (int64_t)t * D + n) + Act<A>::round(acc);
   Act<A>::store(out, (int64_t)t * D + n, acc);
 }
 
@@ -1030,25 +1040,27 @@ hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, 
 }
 
 hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
-                          hipStream_t st) {
+                          hipStream_t st, const void* res) {
   const int T = (int)d.tokens, D = (int)d.hidden, K = (int)d.top_k;
   const bool bf16 = d.act_dtype == KMOE_DTYPE_BF16;
   if (D % 8 == 0) {
     const dim3 grid((D / 8 + 255) / 256, T);
     if (bf16)
       hipLaunchKernelGGL((k_combine8<uint16_t>), grid, dim3(256), 0, st, T, K, D,
-                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out));
+                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out),
+                         reinterpret_cast<const uint16_t*>(res));
     else
       hipLaunchKernelGGL((k_combine8<float>), grid, dim3(256), 0, st, T, K, D, reinterpret_cast<const float*>(y_sorted),
-                         inv, topk_w, reinterpret_cast<float*>(out));
+                         inv, topk_w, reinterpret_cast<float*>(out), reinterpret_cast<const float*>(res));
   } else {
     const dim3 grid((D + 255) / 256, T);
     if (bf16)
       hipLaunchKernelGGL((k_combine1<uint16_t>), grid, dim3(256), 0, st, T, K, D,
-                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out));
+                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out),
+                         reinterpret_cast<const uint16_t*>(res));
     else
       hipLaunchKernelGGL((k_combine1<float>), grid, dim3(256), 0, st, T, K, D, reinterpret_cast<const float*>(y_sorted),
-                         inv, topk_w, reinterpret_cast<float*>(out));
+                         inv, topk_w, reinterpret_cast<float*>(out), reinterpret_cast<const float*>(res));
   }
   return hipGetLastError();
 }

@@ -12,9 +12,18 @@ hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& ro
                         float* topk_w, int32_t* hist, hipStream_t st);
 // Split router (many blocks per token; same logits and selections as
 // launch_route): part holds route_split_part_floats(d) floats of workspace.
+// With a SliceNorm, x is the residual stream h: the router reduces and
+// normalises the rows itself (rms_norm, kappa/qwen3/norms.py:10-16), routes
+// the normalised rows and writes them to h2 for the expert kernels.
+struct SliceNorm {
+  const void* scale;  // [D] RMSNorm scale; NULL: x is routed as given
+  int scale_bf16;
+  float eps;
+  void* h2;  // [T][D] normalised rows (activation dtype)
+};
 size_t route_split_part_floats(const kmoe_desc& d);
 hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part, float* logits,
-                              int32_t* topk_idx, float* topk_w, hipStream_t st);
+                              int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm = nullptr);
 hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const int32_t* hist, int32_t* group_sizes,
                            int32_t* offsets, int32_t* active, int32_t* sorted_token, int32_t* sorted_expert,
                            int32_t* inv, hipStream_t st);
@@ -31,9 +40,15 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
 hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, const int32_t* sorted_token,
                                  const int32_t* sorted_expert, const kmoe_weight* gate, const kmoe_weight* up,
                                  const kmoe_weight* down, void* h_sorted, void* y_sorted, hipStream_t st);
+// out = round(sum_j w * y_sorted[inv]) [+ residual res, rounded again], res may be NULL
 hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
-                          hipStream_t st);
+                          hipStream_t st, const void* res = nullptr);
 hipError_t launch_topk_w_cast(const kmoe_desc& d, const float* topk_w, void* out, hipStream_t st);
+
+// block.hip
+size_t rms_norm_lds_bytes(int64_t D);
+hipError_t launch_rms_norm(const kmoe_desc& d, const void* h, const void* scale, kmoe_dtype scale_dtype, float eps,
+                           void* out, hipStream_t st);
 
 // weights.hip
 hipError_t launch_prepack(const kmoe_desc& d, const kmoe_weight& gate, const kmoe_weight& up, const kmoe_weight& down,

@@ -8,6 +8,7 @@
 
 #include "common.h"
 #include "launch.h"
+#include "norm.h"
 
 namespace kmoe {
 
@@ -358,7 +359,10 @@ __global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int 
 // k_route, computed by many blocks per token instead of one.
 //
 // k_route_slices, block (g, tb): wave w runs the fmaf chain of slice
-// s = 4g + w for the TB tokens tb*TB .. tb*TB+TB-1, a lane owning EPL
+// s = 4g + w for the TB tokens tb*TB .. tb*TB+TB-1 (with a SliceNorm, x is
+// the residual stream and the block first normalises its tokens' rows -
+// rms_norm of kappa/qwen3/norms.py:10-16 - writing its four slices of the
+// normalised rows for the expert kernels), a lane owning EPL
 // consecutive experts (all 64 rows of the slice in flight at once when they
 // fit in 64 registers). The block then applies tree levels st = 1 and 2 to its
 // four slices (the zero-padded tree's aligned group of four) and writes the
@@ -370,19 +374,44 @@ __global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int 
 template <typename A, int RT, int EPL, int TB>
 __global__ __launch_bounds__(256) void k_route_slices(int T, int D, int E, int P, int Q, const A* __restrict__ x,
                                                        const void* __restrict__ rw, const void* __restrict__ rscale,
-                                                       int scale_bf16, int scale_pc, float* __restrict__ part) {
+                                                       int scale_bf16, int scale_pc, float* __restrict__ part,
+                                                       const kmoe_host::SliceNorm nm) {
   using Row = RouterRow<RT, EPL>;
   constexpr int U = Row::kWords <= 1 ? 64 : 64 / Row::kWords;  // rows per load stage
   __shared__ float xs[4][kRouterSlice][TB];
   __shared__ float red[2][TB * EPL][64];
+  __shared__ float rfac[TB];
+  extern __shared__ float nrow[];  // with nm.scale: TB staged rows, norm_row_floats(D) each
   const int g = blockIdx.x, t0 = blockIdx.y * TB;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int s = 4 * g + w;
   const int d0 = s * kRouterSlice;
+  const int NRF = norm_row_floats(D);
+  if (nm.scale) {
+    // x is the residual stream h: wave tt reduces row t0 + tt (the canonical
+    // rms_norm order); the slices are normalised below
+    if (w < TB && t0 + w < T) {
+      const float r = wave_rms_factor(x + (int64_t)(t0 + w) * D, D, nm.eps, nrow + w * NRF);
+      if (lane == 0) rfac[w] = r;
+    }
+    __syncthreads();
+  }
   for (int i = threadIdx.x; i < 4 * kRouterSlice * TB; i += blockDim.x) {
     const int tt = i % TB, r = (i / TB) % kRouterSlice, ws = i / (TB * kRouterSlice);
     const int d = (4 * g + ws) * kRouterSlice + r;
-    xs[ws][r][tt] = (t0 + tt < T && d < D) ? Act<A>::load(x, (int64_t)(t0 + tt) * D + d) : 0.0f;
+    float v = 0.0f;
+    if (t0 + tt < T && d < D) {
+      if (nm.scale) {
+        // the block's input h2 = round_act((h * r) * scale): staged here and
+        // written out for the expert kernels (each block writes its slices)
+        const float sc = load_scale(nm.scale, nm.scale_bf16, d);
+        v = rms_apply<A>(nrow[tt * NRF + (d >> 6) * (kRouterSlice + 1) + (d & 63)], rfac[tt], sc);
+        Act<A>::store(reinterpret_cast<A*>(nm.h2), (int64_t)(t0 + tt) * D + d, v);
+      } else {
+        v = Act<A>::load(x, (int64_t)(t0 + tt) * D + d);
+      }
+    }
+    xs[ws][r][tt] = v;
   }
   const int LPR = (E + EPL - 1) / EPL;
   const int e0 = lane * EPL;
@@ -829,44 +858,49 @@ size_t route_split_part_floats(const kmoe_desc& d) {
 }
 
 template <typename A, int RT, int EPL, int TB>
-static void launch_slices(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part, hipStream_t st) {
+static void launch_slices(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part,
+                          const SliceNorm& nm, hipStream_t st) {
   const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts;
   const int scale_bf16 = (r.dtype == KMOE_DTYPE_I8 && r.scale_dtype == KMOE_DTYPE_BF16) ? 1 : 0;
   const int scale_pc = (r.dtype == KMOE_DTYPE_I8 && r.scale_kind == KMOE_SCALE_CHANNEL) ? 1 : 0;
-  hipLaunchKernelGGL((k_route_slices<A, RT, EPL, TB>), dim3(sh.Q, (T + TB - 1) / TB), dim3(256), 0, st, T, D, E,
-                     sh.P, sh.Q, reinterpret_cast<const A*>(x), r.values, r.scale, scale_bf16, scale_pc, part);
+  const size_t lds = nm.scale ? (size_t)TB * norm_row_floats(D) * sizeof(float) : 0;
+  hipLaunchKernelGGL((k_route_slices<A, RT, EPL, TB>), dim3(sh.Q, (T + TB - 1) / TB), dim3(256), lds, st, T, D, E,
+                     sh.P, sh.Q, reinterpret_cast<const A*>(x), r.values, r.scale, scale_bf16, scale_pc, part, nm);
 }
 
 template <typename A, int RT, int EPL>
-static void slices_tb(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part, hipStream_t st) {
-  if (sh.TB == 1) return launch_slices<A, RT, EPL, 1>(d, sh, x, r, part, st);
-  if (sh.TB == 2) return launch_slices<A, RT, EPL, 2>(d, sh, x, r, part, st);
-  return launch_slices<A, RT, EPL, 4>(d, sh, x, r, part, st);
+static void slices_tb(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part,
+                      const SliceNorm& nm, hipStream_t st) {
+  if (sh.TB == 1) return launch_slices<A, RT, EPL, 1>(d, sh, x, r, part, nm, st);
+  if (sh.TB == 2) return launch_slices<A, RT, EPL, 2>(d, sh, x, r, part, nm, st);
+  return launch_slices<A, RT, EPL, 4>(d, sh, x, r, part, nm, st);
 }
 
 template <typename A, int RT>
-static void slices_epl(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part, hipStream_t st) {
+static void slices_epl(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part,
+                       const SliceNorm& nm, hipStream_t st) {
   switch (sh.EPL) {
     case 1:
-      if constexpr (RT == 0) return slices_tb<A, RT, 1>(d, sh, x, r, part, st);
+      if constexpr (RT == 0) return slices_tb<A, RT, 1>(d, sh, x, r, part, nm, st);
       [[fallthrough]];
     case 2:
-      if constexpr (RT != 2) return slices_tb<A, RT, 2>(d, sh, x, r, part, st);
+      if constexpr (RT != 2) return slices_tb<A, RT, 2>(d, sh, x, r, part, nm, st);
       [[fallthrough]];
     case 4:
-      return slices_tb<A, RT, 4>(d, sh, x, r, part, st);
+      return slices_tb<A, RT, 4>(d, sh, x, r, part, nm, st);
     case 8:
-      return slices_tb<A, RT, 8>(d, sh, x, r, part, st);
+      return slices_tb<A, RT, 8>(d, sh, x, r, part, nm, st);
     default:
-      return slices_tb<A, RT, 16>(d, sh, x, r, part, st);
+      return slices_tb<A, RT, 16>(d, sh, x, r, part, nm, st);
   }
 }
 
 template <typename A>
-static void slices_rt(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part, hipStream_t st) {
-  if (r.dtype == KMOE_DTYPE_F32) return slices_epl<A, 0>(d, sh, x, r, part, st);
-  if (r.dtype == KMOE_DTYPE_BF16) return slices_epl<A, 1>(d, sh, x, r, part, st);
-  return slices_epl<A, 2>(d, sh, x, r, part, st);
+static void slices_rt(const kmoe_desc& d, const SplitShape& sh, const void* x, const kmoe_weight& r, float* part,
+                      const SliceNorm& nm, hipStream_t st) {
+  if (r.dtype == KMOE_DTYPE_F32) return slices_epl<A, 0>(d, sh, x, r, part, nm, st);
+  if (r.dtype == KMOE_DTYPE_BF16) return slices_epl<A, 1>(d, sh, x, r, part, nm, st);
+  return slices_epl<A, 2>(d, sh, x, r, part, nm, st);
 }
 
 template <int EPL>
@@ -879,12 +913,13 @@ static void launch_finish(const kmoe_desc& d, const SplitShape& sh, const float*
 }
 
 hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& r, float* part, float* logits,
-                              int32_t* topk_idx, float* topk_w, hipStream_t st) {
+                              int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm) {
   const SplitShape sh = split_shape(d, r);
+  const SliceNorm nm = norm ? *norm : SliceNorm{nullptr, 0, 0.0f, nullptr};
   if (d.act_dtype == KMOE_DTYPE_BF16)
-    slices_rt<uint16_t>(d, sh, x, r, part, st);
+    slices_rt<uint16_t>(d, sh, x, r, part, nm, st);
   else
-    slices_rt<float>(d, sh, x, r, part, st);
+    slices_rt<float>(d, sh, x, r, part, nm, st);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int E = (int)d.num_experts;

@@ -1,4 +1,4 @@
-"""Qwen3 MoE block API mirroring kappa.qwen3 (ffn_moe, quant, architecture)."""
+"""Qwen3 MoE block API mirroring kappa.qwen3 (ffn_moe, quant, architecture, norms, block)."""
 
 from .architecture import (
     MoEImpl,
@@ -7,6 +7,7 @@ from .architecture import (
     qwen3_235b_a22b_moe_config,
     qwen3_config_for_preset,
 )
+from .block import moe_block_ffn, rms_norm
 from .ffn_moe import PackedExperts, moe_swiglu_ffn, moe_swiglu_ffn_legacy, prepack_moe_experts
 from .quant import (
     Q8Weight,
@@ -25,6 +26,7 @@ __all__ = [
     "Qwen3Config",
     "Weight",
     "is_q8_weight",
+    "moe_block_ffn",
     "moe_layer_config",
     "moe_swiglu_ffn",
     "moe_swiglu_ffn_legacy",
@@ -33,6 +35,7 @@ __all__ = [
     "quantize_weight_per_channel",
     "qwen3_235b_a22b_moe_config",
     "qwen3_config_for_preset",
+    "rms_norm",
     "to_compute_dtype",
     "weight_param_dtype",
 ]

@@ -198,6 +198,17 @@ def _route_checks(x: torch.Tensor, router_w: Weight, num_experts: int) -> tuple[
     return b, t, d
 
 
+def _norm_scale(scale: torch.Tensor, d: int, dev: torch.device) -> torch.Tensor:
+    """The RMSNorm scale as a contiguous [D] f32 or bf16 tensor on ``dev``."""
+    if not isinstance(scale, torch.Tensor):
+        raise ValueError("the norm scale must be a tensor")
+    if scale.numel() != d:
+        raise ValueError(f"norm scale has {scale.numel()} entries, hidden size is {d}")
+    if scale.dtype not in (torch.bfloat16, torch.float32):
+        scale = scale.to(torch.float32)
+    return scale.reshape(d).to(dev).contiguous()
+
+
 def _moe_forward(
     x: torch.Tensor,
     router_w: Weight,
@@ -211,7 +222,10 @@ def _moe_forward(
     packed: PackedExperts | None,
     return_routing: bool = False,
     capacity: int = 0,
+    norm: tuple[torch.Tensor, float] | None = None,
 ):
+    """The block through the C ABI. With ``norm = (scale, epsilon)``, ``x`` is the
+    residual stream h and the call returns h + block(rms_norm(h)) (kmoe_forward_block)."""
     b, t, d = _route_checks(x, router_w, num_experts)
     if x.device.type != "cuda":
         raise ValueError(f"x must be on a HIP device (got {x.device}); the block has no CPU implementation")
@@ -246,16 +260,21 @@ def _moe_forward(
     if return_routing:
         idx = torch.empty((T, K), dtype=torch.int32, device=dev)
         w_out = torch.empty((T, K), dtype=x.dtype, device=dev)
-    _lib.check(
-        L.kmoe_forward(
-            desc, x_flat.data_ptr(), r, g, u, dn,
-            packed.struct() if packed is not None else None,
-            out.data_ptr(),
-            idx.data_ptr() if idx is not None else None,
-            w_out.data_ptr() if w_out is not None else None,
-            ws.data_ptr(), ws.numel(), stream,
+    pk = packed.struct() if packed is not None else None
+    idx_p = idx.data_ptr() if idx is not None else None
+    w_p = w_out.data_ptr() if w_out is not None else None
+    if norm is None:
+        st = L.kmoe_forward(
+            desc, x_flat.data_ptr(), r, g, u, dn, pk, out.data_ptr(), idx_p, w_p, ws.data_ptr(), ws.numel(), stream
         )
-    )  # fmt: skip
+    else:
+        scale, eps = norm
+        scale = _norm_scale(scale, d, dev)
+        st = L.kmoe_forward_block(
+            desc, x_flat.data_ptr(), scale.data_ptr(), kmoe_dtype(scale.dtype), float(eps), r, g, u, dn, pk,
+            out.data_ptr(), idx_p, w_p, ws.data_ptr(), ws.numel(), stream,
+        )  # fmt: skip
+    _lib.check(st)
     out = out.reshape(b, t, d)
     if return_routing:
         return out, idx, w_out

@@ -24,6 +24,9 @@ Function -> reference it restates:
   capacity_slots  kappa/qwen3/ffn_moe.py:23-31, 136-141 (c_buf and c_dyn)
   drop_over_capacity  kappa/qwen3/ffn_moe.py:59-71, 141, 153 (slot within expert, mask)
   quantize_*      kappa/qwen3/quant.py:41-48
+  rms_norm        kappa/qwen3/norms.py:10-16 (squares summed in the router's slice order)
+  residual_add    kappa/qwen3/block.py:207 (h + out)
+  forward_block   kappa/qwen3/block.py:196-207 (rms_norm -> moe_swiglu_ffn -> residual)
 """
 
 from __future__ import annotations
@@ -72,6 +75,7 @@ def lib() -> ctypes.CDLL:
             _f32p,
         ] * 3 + [_f32p, _f32p]
         L.orc_combine.argtypes = [_i64, _i64, _i64, ctypes.c_int, _f32p, _i32p, _f32p, _f32p]
+        L.orc_rms_norm.argtypes = [_i64, _i64, ctypes.c_int, _f32p, _f32p, ctypes.c_float, _f32p]
         L.orc_quantize_per_channel.argtypes = [_i64, _i64, _i64, _f32p, _i8p, _f32p]
         L.orc_quantize_per_tensor.restype = ctypes.c_float
         L.orc_quantize_per_tensor.argtypes = [_i64, _f32p, _i8p]
@@ -234,6 +238,32 @@ def forward(x, router, gate, up, down, *, k: int, act_bf16: bool, capacity: int 
     h, y = expert_ffn(x, disp["offsets"], disp["sorted_token"], gate, up, down, act_bf16)
     out = combine(y, disp["inv"], w, act_bf16)
     return {"logits": logits, "idx": idx, "w": w, **disp, "h_sorted": h, "y_sorted": y, "out": out}
+
+
+def rms_norm(h, scale, eps: float, act_bf16: bool) -> np.ndarray:
+    """R1: rms_norm(h, scale, epsilon=eps) (kappa/qwen3/norms.py:10-16) in the
+    canonical order, rounded to the activation dtype."""
+    h = _f32(h)
+    scale = _f32(scale).reshape(-1)
+    T, D = h.shape
+    if scale.shape[0] != D:
+        raise ValueError(f"scale has {scale.shape[0]} entries, hidden size is {D}")
+    out = np.empty((T, D), np.float32)
+    lib().orc_rms_norm(T, D, int(act_bf16), _p(h, _f32p), _p(scale, _f32p), float(eps), _p(out, _f32p))
+    return out
+
+
+def residual_add(h, moe_out, act_bf16: bool) -> np.ndarray:
+    """R2: round_act(f32(h) + f32(moe_out)) (the ``h + out`` of kappa/qwen3/block.py:207)."""
+    s = (_f32(h) + _f32(moe_out)).astype(np.float32)
+    return bf16_round(s) if act_bf16 else s
+
+
+def forward_block(h, norm_scale, router, gate, up, down, *, k: int, act_bf16: bool, eps: float = 1e-6) -> dict:
+    """h + moe_swiglu_ffn(rms_norm(h, norm_scale)) (kappa/qwen3/block.py:196-207)."""
+    h2 = rms_norm(h, norm_scale, eps, act_bf16)
+    moe = forward(h2, router, gate, up, down, k=k, act_bf16=act_bf16)
+    return {**moe, "h2": h2, "moe_out": moe["out"], "out": residual_add(h, moe["out"], act_bf16)}
 
 
 def quantize_per_channel(w):

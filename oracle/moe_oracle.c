@@ -33,6 +33,16 @@
  * round_act is the identity for f32 activations and round-to-nearest-even to
  * bfloat16 for bf16 activations. Every bf16 value is carried in a float.
  *
+ * Around the block (the steps on either side of it in a Qwen3 MoE layer,
+ * kappa/qwen3/block.py:196-207):
+ *  R1 h2 = rms_norm(h, scale, eps) (kappa/qwen3/norms.py:10-16):
+ *     S = sum_d f32(h_d)*f32(h_d) with every square rounded to float and the
+ *     sum in the N0 order (slices of 64, each a sequential chain of adds from
+ *     +0.0f, slice sums combined by the zero-padded pairwise tree);
+ *     var = S / D; r = 1 / sqrtf(var + eps) (IEEE division and square root);
+ *     h2_d = round_act((f32(h_d) * r) * f32(scale_d)).
+ *  R2 out = round_act(f32(h) + f32(moe_out)), moe_out already round_act.
+ *
  * Each output element is produced by exactly one thread in a fixed order, so
  * results do not depend on the OpenMP thread count.
  */
@@ -302,6 +312,42 @@ void orc_combine(int64_t T, int64_t K, int64_t D, int round_bf16, const float* y
       }
       out[t * D + n] = round_bf16 ? bf16r(acc) : acc;
     }
+  }
+}
+
+/* R1: rms_norm of each row of h [T][D] (kappa/qwen3/norms.py:10-16). */
+void orc_rms_norm(int64_t T, int64_t D, int round_bf16, const float* h, const float* scale, float eps, float* out) {
+  const int64_t S = (D + ORC_SLICE - 1) / ORC_SLICE;
+  int64_t P = 1;
+  while (P < S) P <<= 1;
+#pragma omp parallel
+  {
+    float* part = (float*)calloc((size_t)P, sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < T; ++t) {
+      const float* row = h + t * D;
+      for (int64_t s = 0; s < P; ++s) {
+        float acc = 0.0f;
+        if (s < S) {
+          const int64_t d1 = (s + 1) * ORC_SLICE < D ? (s + 1) * ORC_SLICE : D;
+          for (int64_t d = s * ORC_SLICE; d < d1; ++d) {
+            const float sq = row[d] * row[d];
+            acc = acc + sq;
+          }
+        }
+        part[s] = acc;
+      }
+      for (int64_t st = 1; st < P; st <<= 1)
+        for (int64_t i = 0; i + st < P; i += 2 * st) part[i] = part[i] + part[i + st];
+      const float var = part[0] / (float)D;
+      const float r = 1.0f / sqrtf(var + eps);
+      for (int64_t d = 0; d < D; ++d) {
+        const float n = row[d] * r;
+        const float v = n * scale[d];
+        out[t * D + d] = round_bf16 ? bf16r(v) : v;
+      }
+    }
+    free(part);
   }
 }
 

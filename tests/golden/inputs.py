@@ -162,3 +162,22 @@ CAPACITY_SPECS = [
     (Spec("cap_f32_slots", T=24, D=64, E=8, K=2, I=32, act="f32", weights="f32", router="f32", base_seed=80), 1.25, 3),
     (Spec("cap_skew_bf16", T=48, D=128, E=16, K=2, I=64, skew_lambda=1.0, base_seed=90), 1.0, None),
 ]
+
+
+# The MoE block with the steps either side of it (kappa/qwen3/block.py:196-207):
+# (spec, epsilon). The spec's x is the residual stream h; the RMSNorm scale
+# (pre_ffn_norm, seed 7) is N(1, 0.1), rounded to bf16 for bf16 activations.
+#   blk_w8c_bf16:  the 30B numerics at toy size
+#   blk_d192_k8:   hidden 192 (three slices: a zero-padded sum tree), top-8
+#   blk_toy_f32:   the fp32 toy block
+BLOCK_SPECS = [
+    (Spec("blk_w8c_bf16", T=32, D=128, E=16, K=4, I=64, base_seed=100), 1e-6),
+    (Spec("blk_d192_k8", T=24, D=192, E=32, K=8, I=96, base_seed=110), 1e-5),
+    (Spec("blk_toy_f32", T=16, D=256, E=8, K=2, I=128, act="f32", weights="f32", router="f32", base_seed=120), 1e-6),
+]
+
+
+def make_norm_scale(spec: Spec) -> np.ndarray:
+    """pre_ffn_norm [D]: N(1, 0.1) from seed 7 (+ base_seed), bf16 for bf16 activations."""
+    s = (_normal(7 + spec.base_seed, (spec.D,), 0.1) + np.float32(1.0)).astype(np.float32)
+    return bf16_rne(s) if spec.act == "bf16" else s

@@ -12,6 +12,8 @@ checked against an independent restatement:
   _moe_ragged order  kappa/qwen3/ffn_moe.py:189-200, 212 (argsort stable, bincount, inv)
   _moe_fixed_capacity kappa/qwen3/ffn_moe.py:107-158 with _slot_within_expert :59-71
                      and _fixed_capacity_buffer_slots :23-31 (token dropping)
+  rms_norm           kappa/qwen3/norms.py:10-16
+  block MoE half     kappa/qwen3/block.py:196-207 (h2 = rms_norm(h); h + moe(h2))
 
 Accumulations run in float64 and are rounded to the activation dtype at the
 points where the reference's arrays carry ``x.dtype``; bf16 rounding uses
@@ -32,7 +34,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
-from inputs import CAPACITY_SPECS, GOLDEN_SPECS, Spec, digest, make_inputs  # noqa: E402
+from inputs import BLOCK_SPECS, CAPACITY_SPECS, GOLDEN_SPECS, Spec, digest, make_inputs, make_norm_scale  # noqa: E402
 
 
 def as_act(a, act: str) -> np.ndarray:
@@ -181,6 +183,25 @@ def reference_fixed_capacity(spec: Spec, inp: dict, blk: dict, cf: float, fixed_
     }
 
 
+def reference_rms_norm(h: np.ndarray, scale: np.ndarray, eps: float, act: str) -> np.ndarray:
+    """kappa/qwen3/norms.py:10-16: xf = f32(h); var = mean(xf^2); (xf * rsqrt(var + eps)) * f32(scale),
+    cast to the activation dtype (float64 arithmetic)."""
+    xf = h.astype(np.float64)
+    var = np.mean(xf * xf, axis=-1, keepdims=True)
+    normed = xf / np.sqrt(var + eps)
+    return as_act(normed * scale.astype(np.float64), act)
+
+
+def reference_block_residual(spec: Spec, inp: dict, scale: np.ndarray, eps: float) -> dict:
+    """h2 = rms_norm(h); out = h + moe_swiglu_ffn(h2) in the activation dtype (kappa/qwen3/block.py:196-207)."""
+    h = inp["x"]
+    h2 = reference_rms_norm(h, scale, eps, spec.act)
+    moe = reference_block(spec, {**inp, "x": h2})
+    out = as_act(h.astype(np.float64) + moe["out"].astype(np.float64), spec.act)
+    return {"h2": h2.astype(np.float32), "idx": moe["idx"], "w": moe["w"], "gap": moe["gap"],
+            "moe_out": moe["out"], "out": out.astype(np.float32)}  # fmt: skip
+
+
 def main() -> None:
     meta = {}
     for spec in GOLDEN_SPECS:
@@ -205,6 +226,18 @@ def main() -> None:
             "dropped": dropped,
         }
         print(f"{spec.name}: capacity {int(ref['capacity'])}, {dropped} of {spec.T * spec.K} assignments dropped")
+    for spec, eps in BLOCK_SPECS:
+        inp = make_inputs(spec)
+        scale = make_norm_scale(spec)
+        ref = reference_block_residual(spec, inp, scale, eps)
+        np.savez_compressed(os.path.join(HERE, f"{spec.name}.npz"), norm_scale=scale, **ref)
+        meta[spec.name] = {
+            "spec": spec.as_dict(),
+            "input_sha256": digest({**inp, "norm_scale": scale}),
+            "min_gap": float(np.min(ref["gap"])),
+            "epsilon": eps,
+        }
+        print(f"{spec.name}: T={spec.T} D={spec.D} eps={eps} min_gap={np.min(ref['gap']):.3e}")
     with open(os.path.join(HERE, "golden.json"), "w") as f:
         json.dump(meta, f, indent=1, sort_keys=True)
 

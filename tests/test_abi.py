@@ -159,3 +159,35 @@ def test_zero_tokens_is_a_no_op_after_validation():
     # T = 0 still validates, then reports the missing device (no launch is attempted)
     st = L.kmoe_forward(desc(T=0), 1, f, w, w, w, None, 1, None, None, None, 0, None)
     assert st == _lib.ERR_NO_DEVICE
+
+
+def test_block_and_norm_entry_points_validate_before_any_hip_call():
+    L = _lib.lib()
+    d = desc()
+    w = weight()
+    f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
+    BF = _lib.DTYPE_BF16
+    cases = [
+        (dict(scale=None), _lib.ERR_INVALID_ARG, "norm scale pointer"),
+        (dict(sdt=_lib.DTYPE_I8), _lib.ERR_INVALID_ARG, "norm scale dtype"),
+        (dict(eps=-1.0), _lib.ERR_INVALID_ARG, "epsilon"),
+        (dict(eps=float("nan")), _lib.ERR_INVALID_ARG, "epsilon"),
+        (dict(h=None), _lib.ERR_INVALID_ARG, "h and out"),
+        (dict(out=7), _lib.ERR_INVALID_ARG, "alias"),
+        (dict(ws=None), _lib.ERR_WORKSPACE_TOO_SMALL, "workspace"),
+        (dict(router=weight(values=None)), _lib.ERR_INVALID_ARG, "router values"),
+    ]
+    for over, want, frag in cases:
+        a = dict(h=7, scale=1, sdt=BF, eps=1e-6, router=f, out=9, ws=1)
+        a.update(over)
+        st = L.kmoe_forward_block(d, a["h"], a["scale"], a["sdt"], a["eps"], a["router"], w, w, w, None, a["out"],
+                                  None, None, a["ws"], 1 << 40, None)  # fmt: skip
+        msg = L.kmoe_last_error().decode()
+        assert st == want and frag in msg, (over, st, msg)
+    assert L.kmoe_rms_norm(d, 1, None, BF, 1e-6, 2, None) == _lib.ERR_INVALID_ARG
+    assert L.kmoe_rms_norm(d, 1, 1, _lib.DTYPE_I8, 1e-6, 2, None) == _lib.ERR_INVALID_ARG
+    assert L.kmoe_rms_norm(d, None, 1, BF, 1e-6, 2, None) == _lib.ERR_INVALID_ARG
+    if not gpu_available():
+        assert L.kmoe_rms_norm(d, 1, 1, BF, 1e-6, 2, None) == _lib.ERR_NO_DEVICE
+        st = L.kmoe_forward_block(d, 7, 1, BF, 1e-6, f, w, w, w, None, 9, None, None, 1, 1 << 40, None)
+        assert st == _lib.ERR_NO_DEVICE

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from inputs import GOLDEN_SPECS, digest, make_inputs
+from inputs import BLOCK_SPECS, GOLDEN_SPECS, digest, make_inputs, make_norm_scale
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 META = json.load(open(os.path.join(HERE, "golden.json")))
@@ -116,3 +116,32 @@ def test_oracle_fixed_capacity_matches_golden(case):
     else:
         scale = max(float(np.abs(g["out"]).max()), 1e-30)
         assert np.max(np.abs(r["out"] - g["out"])) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("case", BLOCK_SPECS, ids=[c[0].name for c in BLOCK_SPECS])
+def test_oracle_block_with_norm_and_residual_matches_golden(case):
+    """h + moe_swiglu_ffn(rms_norm(h)) (kappa/qwen3/block.py:196-207, norms.py:10-16)."""
+    spec, eps = case
+    inp = make_inputs(spec)
+    scale = make_norm_scale(spec)
+    assert digest({**inp, "norm_scale": scale}) == META[spec.name]["input_sha256"]
+    g = np.load(os.path.join(HERE, f"{spec.name}.npz"))
+    bf16 = spec.act == "bf16"
+    r = oracle.forward_block(inp["x"], scale, inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K,
+                             act_bf16=bf16, eps=eps)  # fmt: skip
+    # the normalised input: fp32 in the canonical order vs fp64, so a rare one-ulp
+    # flip of the final rounding (bf16: 2^-8 relative; fp32: a few ulps)
+    d = np.abs(r["h2"] - g["h2"])
+    if bf16:
+        assert np.mean(d > 0) < 2e-3
+        assert np.all(d <= 2.0**-8 * np.abs(g["h2"]) + 1e-30)
+    else:
+        assert np.all(d <= 4 * np.finfo(np.float32).eps * np.abs(g["h2"]) + 1e-30)
+    np.testing.assert_array_equal(r["idx"], g["idx"])
+    for a, b in ((r["moe_out"], g["moe_out"]), (r["out"], g["out"])):
+        if bf16:
+            diff = np.abs(a - b)
+            assert np.mean(diff > 0) < 5e-3
+            assert np.all(diff <= 2.0**-7 * np.abs(b) + 1e-6)
+        else:
+            assert np.max(np.abs(a - b)) <= 1e-5 * max(float(np.abs(b).max()), 1e-30)

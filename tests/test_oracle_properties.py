@@ -339,3 +339,75 @@ def test_dropped_assignments_remove_exactly_their_term():
     # tokens with nothing dropped are bit-identical to the dropless output
     keep_all = ~dropped.any(axis=1)
     np.testing.assert_array_equal(b["out"][keep_all], a["out"][keep_all])
+
+
+# --- rms_norm and the residual (kappa/qwen3/norms.py:10-16, block.py:196-207) ----
+
+
+@pytest.mark.parametrize("c", [1.0, -4.0, 0.5])
+def test_rms_norm_of_a_constant_row_is_its_sign(c):
+    # var = c^2 exactly, r = 1/|c| exactly (powers of two): out = sign(c) * scale
+    h = np.full((3, 128), c, np.float32)
+    out = oracle.rms_norm(h, np.ones(128, np.float32), 0.0, False)
+    np.testing.assert_array_equal(out, np.full_like(h, np.sign(c)))
+
+
+def test_rms_norm_epsilon_is_added_to_the_mean_square():
+    # var = 1 and eps = 1: r = 1 / sqrt(2) (not 1/sqrt(1) + 1, not 1/(1 + 1))
+    h = np.ones((1, 64), np.float32)
+    out = oracle.rms_norm(h, np.ones(64, np.float32), 1.0, False)
+    want = np.float32(1.0) / np.sqrt(np.float32(2.0))
+    np.testing.assert_array_equal(out, np.full_like(h, want))
+
+
+def test_rms_norm_is_invariant_to_power_of_two_scaling_and_scales_per_channel():
+    rng = np.random.default_rng(3)
+    h = rng.standard_normal((5, 192)).astype(np.float32)
+    scale = rng.standard_normal(192).astype(np.float32)
+    a = oracle.rms_norm(h, scale, 0.0, False)
+    np.testing.assert_array_equal(oracle.rms_norm(h * np.float32(4.0), scale, 0.0, False), a)
+    onehot = np.zeros(192, np.float32)
+    onehot[17] = 2.0
+    b = oracle.rms_norm(h, onehot, 0.0, False)
+    np.testing.assert_array_equal(b[:, 17], oracle.rms_norm(h, np.ones(192, np.float32), 0.0, False)[:, 17] * 2)
+    assert not np.any(np.delete(b, 17, axis=1))
+
+
+@pytest.mark.parametrize("D", [16, 100, 2048])
+def test_rms_norm_within_float32_rounding_of_float64(D):
+    rng = np.random.default_rng(D)
+    h = (rng.standard_normal((7, D)) * rng.uniform(0.01, 10.0, (7, 1))).astype(np.float32)
+    scale = (1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    out = oracle.rms_norm(h, scale, 1e-6, False)
+    hf = h.astype(np.float64)
+    ref = hf / np.sqrt(np.mean(hf * hf, axis=1, keepdims=True) + 1e-6) * scale
+    assert np.all(np.abs(out - ref) <= 8 * np.finfo(np.float32).eps * np.abs(ref) + 1e-30)
+
+
+def test_rms_norm_bf16_output_is_rounded():
+    rng = np.random.default_rng(4)
+    h = oracle.bf16_round(rng.standard_normal((4, 64)).astype(np.float32))
+    scale = oracle.bf16_round((1 + 0.1 * rng.standard_normal(64)).astype(np.float32))
+    a = oracle.rms_norm(h, scale, 1e-6, True)
+    np.testing.assert_array_equal(a, oracle.bf16_round(oracle.rms_norm(h, scale, 1e-6, False)))
+
+
+@pytest.mark.parametrize("act_bf16", [False, True])
+def test_block_with_zero_norm_scale_returns_the_residual(act_bf16):
+    # rms_norm(h) * 0 = 0 -> all-equal logits, g = u = 0, h = silu(0) * 0 = 0, y = 0:
+    # the block adds exactly zero, so out == h (a residual dropped or added twice fails)
+    rng = np.random.default_rng(5)
+    T, D, E, K, I = 6, 64, 8, 2, 32
+    h = rng.standard_normal((T, D)).astype(np.float32)
+    if act_bf16:
+        h = oracle.bf16_round(h)
+    router = (0.02 * rng.standard_normal((D, E))).astype(np.float32)
+    gate, up = (0.02 * rng.standard_normal((2, E, D, I))).astype(np.float32)
+    down = (0.02 * rng.standard_normal((E, I, D))).astype(np.float32)
+    r = oracle.forward_block(h, np.zeros(D, np.float32), router, gate, up, down, k=K, act_bf16=act_bf16)
+    np.testing.assert_array_equal(r["idx"], np.tile(np.arange(K, dtype=np.int32), (T, 1)))
+    np.testing.assert_array_equal(r["out"], h)
+    # and with nonzero norm but zero down weights the block output is zero too
+    r2 = oracle.forward_block(h, np.ones(D, np.float32), router, gate, up, np.zeros_like(down), k=K, act_bf16=act_bf16)
+    assert not np.any(r2["moe_out"])
+    np.testing.assert_array_equal(r2["out"], h)
