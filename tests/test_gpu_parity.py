@@ -295,6 +295,36 @@ def test_ragged_token_counts(dev, T):
         check_out(bf16_np(out.reshape(T, 128)), ref["out"], True)
 
 
+@pytest.mark.parametrize(
+    "spec",
+    [
+        Spec("odd_e_bf16", T=5, D=100, E=9, K=3, I=32, base_seed=150),  # E % 2 != 0: per-element router loads
+        Spec("tiny_e_f32", T=3, D=64, E=3, K=1, I=32, act="f32", weights="f32", router="f32", base_seed=151),
+        Spec("e33_qrouter", T=17, D=192, E=33, K=4, I=64, router="w8t", scale_dtype="bf16", base_seed=152),
+        Spec("wide_d_bf16", T=9, D=4096, E=64, K=6, I=64, base_seed=153),  # 64 slices: Q = 16 groups
+        Spec("e200_bf16", T=40, D=256, E=200, K=8, I=32, base_seed=154),  # four experts per lane in the finish
+    ],
+    ids=lambda s: s.name,
+)
+def test_split_router_shapes_match_oracle(dev, spec):
+    """The whole-block call at T <= 64 routes with the split router: top-k
+    indices bit-exact against the oracle (its canonical order) and the output
+    within tolerance, on shapes that take its less common paths."""
+    from kappa_amd.qwen3.ffn_moe import _moe_forward
+
+    inp = make_inputs(spec)
+    bf16 = spec.act == "bf16"
+    x, r, (g, u, d) = spec_to_dev(spec, inp, dev)
+    out, idx, w = _moe_forward(
+        x.reshape(1, spec.T, spec.D), r, g, u, d, num_experts=spec.E, num_experts_per_tok=spec.K,
+        decode_threshold=64, packed=None, return_routing=True,
+    )  # fmt: skip
+    ref = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=bf16)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref["idx"])
+    np.testing.assert_array_equal(w.float().cpu().numpy(), ref["w"])
+    check_out(out.reshape(spec.T, spec.D).float().cpu().numpy(), ref["out"], bf16)
+
+
 # --- weights ------------------------------------------------------------------
 
 
