@@ -373,15 +373,23 @@ def main():
     }
     result["layer_hbm_frac"] = result["layer_hbm_gbs"] / HBM_PEAK_GBS
 
-    # the steps either side of the block: rms_norm in, residual add out
+    # the steps either side of the block: rms_norm in, residual add out. The
+    # fused call, the three separate calls and the bare MoE layer are timed in
+    # interleaved rounds (the clock drifts over a run); medians are reported.
     scale = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
-    fused_s = time_block(bounds, xs, outs, scale, args.steps, args.warmup, fused=True)
-    sep_s = time_block(bounds, xs, outs, scale, args.steps, args.warmup, fused=False)
+    rounds = {"fused": [], "separate": [], "moe_only": []}
+    n_round = max(args.steps // 5, 5)
+    for _ in range(5):
+        rounds["fused"].append(time_block(bounds, xs, outs, scale, n_round, 2, fused=True) / n_round)
+        rounds["separate"].append(time_block(bounds, xs, outs, scale, n_round, 2, fused=False) / n_round)
+        rounds["moe_only"].append(time_forward(bounds, xs, outs, n_round, 2) / n_round)
+    med = {k: sorted(v)[len(v) // 2] * 1e6 for k, v in rounds.items()}
     result["block"] = {
         "workload": f"h + moe_layer(rms_norm(h)), decode T={T}",
-        "fused_us_per_step": fused_s * 1e6 / args.steps,
-        "separate_us_per_step": sep_s * 1e6 / args.steps,
-        "moe_only_us_per_step": ms_step * 1e3,
+        "fused_us_per_step": med["fused"],
+        "separate_us_per_step": med["separate"],
+        "moe_only_us_per_step": med["moe_only"],
+        "rounds": f"5 interleaved rounds of {n_round} steps, medians",
     }
     log(f"bench: block {result['block']}")
 
