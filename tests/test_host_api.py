@@ -82,3 +82,22 @@ def test_fixed_capacity_slots_follow_reference_formula():
     assert _fixed_capacity(c_he, 11) == 3  # 1.25 * 22 / 8 = 3.4375
     c_he2 = dataclasses.replace(c_he, moe_capacity_factor=1.75)
     assert _fixed_capacity(c_he2, 8) == 4  # 1.75 * 16 / 8 = 3.5
+
+
+def test_block_api_mirrors_the_moe_errors_and_rejects_cpu_tensors():
+    from kappa_amd.qwen3 import moe_block_ffn, rms_norm
+
+    x, r, g, u, d = args()
+    scale = torch.ones(16)
+    with pytest.raises(ValueError, match="moe_swiglu_ffn requires cfg.use_moe"):
+        moe_block_ffn(x, scale, r, g, u, d, cfg=cfg(use_moe=False))
+    with pytest.raises(ValueError, match="unknown moe_impl"):
+        moe_block_ffn(x, scale, r, g, u, d, cfg=cfg(moe_impl="bogus", moe_ragged_decode_token_threshold=0))
+    with pytest.raises(ValueError, match=r"router_w shape \(16, 4\) != \(16, 8\)"):
+        moe_block_ffn(x, scale, torch.zeros(16, 4), g, u, d, cfg=cfg())
+    with pytest.raises(ValueError, match="HIP device"):
+        moe_block_ffn(x, scale, r, g, u, d, cfg=cfg())
+    with pytest.raises(ValueError, match="HIP device"):
+        rms_norm(x, scale)
+    with pytest.raises(ValueError, match="out_dtype"):
+        rms_norm(x, scale, out_dtype=torch.float16)
