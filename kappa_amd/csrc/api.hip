@@ -349,10 +349,15 @@ kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host
   void* ys = base + w.y_sorted;
   if (desc->tokens <= kmoe::kDispatchBlock) {
     // one 64-token chunk: the split router (normalising its input rows when
-    // there is a norm); the dispatch counts the chunk itself
+    // there is a norm, and running the dispatch sort itself at T <= 4); the
+    // dispatch counts the chunk itself
     float* part = reinterpret_cast<float*>(base + w.route_part);
-    KMOE_HIP(kmoe_host::launch_route_split(*desc, x, *router, part, nullptr, tidx, tw, st, norm), "route kernels");
-    KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, nullptr, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
+    const kmoe_host::DispatchOut dout{gs, off, act, stok, sexp, inv};
+    KMOE_HIP(kmoe_host::launch_route_split(*desc, x, *router, part, nullptr, tidx, tw, st, norm, &dout),
+             "route kernels");
+    if (!kmoe_host::split_router_dispatches(*desc))
+      KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, nullptr, gs, off, act, stok, sexp, inv, st),
+               "dispatch kernel");
   } else {
     if (norm)
       KMOE_HIP(kmoe_host::launch_rms_norm(*desc, x, norm->scale, norm->scale_bf16 ? KMOE_DTYPE_BF16 : KMOE_DTYPE_F32,

@@ -21,9 +21,22 @@ struct SliceNorm {
   float eps;
   void* h2;  // [T][D] normalised rows (activation dtype)
 };
+// The dispatch sort's outputs (as launch_dispatch). Given to the split router,
+// it runs the sort itself when the tokens fit one finish block (T <= 4;
+// split_router_dispatches(d)), and the caller skips launch_dispatch.
+struct DispatchOut {
+  int32_t* group_sizes;
+  int32_t* offsets;
+  int32_t* active;
+  int32_t* sorted_token;
+  int32_t* sorted_expert;
+  int32_t* inv;
+};
+inline bool split_router_dispatches(const kmoe_desc& d) { return d.tokens <= 4; }
 size_t route_split_part_floats(const kmoe_desc& d);
 hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part, float* logits,
-                              int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm = nullptr);
+                              int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm = nullptr,
+                              const DispatchOut* dispatch = nullptr);
 hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const int32_t* hist, int32_t* group_sizes,
                            int32_t* offsets, int32_t* active, int32_t* sorted_token, int32_t* sorted_expert,
                            int32_t* inv, hipStream_t st);

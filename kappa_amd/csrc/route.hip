@@ -500,14 +500,14 @@ __global__ __launch_bounds__(256) void k_route_slices(int T, int D, int E, int P
   }
 }
 
+// Finish of token t by one wave: the remaining tree levels and the top-k;
+// idx_lds (may be NULL) also receives the selections.
 template <int EPL>
-__global__ __launch_bounds__(256) void k_route_finish(int T, int E, int K, int Q, const float* __restrict__ part,
-                                                       float* __restrict__ logits, int32_t* __restrict__ topk_idx,
-                                                       float* __restrict__ topk_w, int out_bf16) {
-  __shared__ TopkLds tk[4];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + w;
-  if (t >= T) return;  // per wave: this kernel has no block-wide barrier
+__device__ __forceinline__ void finish_token(int t, int E, int K, int Q, const float* __restrict__ part,
+                                             float* __restrict__ logits, int32_t* __restrict__ topk_idx,
+                                             float* __restrict__ topk_w, int out_bf16, int32_t* idx_lds,
+                                             TopkLds& tk) {
+  const int lane = threadIdx.x & 63;
   float v[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
@@ -525,7 +525,18 @@ __global__ __launch_bounds__(256) void k_route_finish(int T, int E, int K, int Q
     v[i] = (e < E && l == l) ? l : -INFINITY;
     if (logits && e < E) logits[(int64_t)t * E + e] = l;
   }
-  wave_topk<EPL>(t, E, K, v, topk_idx, topk_w, out_bf16, nullptr, tk[w]);
+  wave_topk<EPL>(t, E, K, v, topk_idx, topk_w, out_bf16, idx_lds, tk);
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route_finish(int T, int E, int K, int Q, const float* __restrict__ part,
+                                                       float* __restrict__ logits, int32_t* __restrict__ topk_idx,
+                                                       float* __restrict__ topk_w, int out_bf16) {
+  __shared__ TopkLds tk[4];
+  const int w = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + w;
+  if (t >= T) return;  // per wave: this kernel has no block-wide barrier
+  finish_token<EPL>(t, E, K, Q, part, logits, topk_idx, topk_w, out_bf16, nullptr, tk[w]);
 }
 
 // ---------------------------------------------------------------------------
@@ -706,6 +717,24 @@ __device__ void dispatch_chunk(int T, int E, int K, int b, int nblk, const int32
       }
     }
   }
+}
+
+// T <= 4: the finish is one block, so it also runs the dispatch sort of its
+// tokens (the selections pass through LDS; no second kernel).
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route_finish_dispatch(
+    int T, int E, int K, int Q, const float* __restrict__ part, float* __restrict__ logits,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w, int out_bf16, int32_t* __restrict__ group_sizes,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ active, int32_t* __restrict__ sorted_token,
+    int32_t* __restrict__ sorted_expert, int32_t* __restrict__ inv, int cap) {
+  __shared__ TopkLds tk[4];
+  __shared__ DispatchLds L;
+  __shared__ int32_t idx_lds[4 * kMaxTopK];
+  const int w = threadIdx.x >> 6;
+  if (w < T) finish_token<EPL>(w, E, K, Q, part, logits, topk_idx, topk_w, out_bf16, idx_lds, tk[w]);
+  __syncthreads();
+  dispatch_chunk(T, E, K, 0, 1, idx_lds, nullptr, group_sizes, offsets, active, sorted_token, sorted_expert, inv, cap,
+                 L);
 }
 
 __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, int nblk,
@@ -905,15 +934,23 @@ static void slices_rt(const kmoe_desc& d, const SplitShape& sh, const void* x, c
 
 template <int EPL>
 static void launch_finish(const kmoe_desc& d, const SplitShape& sh, const float* part, float* logits,
-                          int32_t* topk_idx, float* topk_w, hipStream_t st) {
+                          int32_t* topk_idx, float* topk_w, const DispatchOut* ds, hipStream_t st) {
   const int T = (int)d.tokens, E = (int)d.num_experts, K = (int)d.top_k;
   const int out_bf16 = d.act_dtype == KMOE_DTYPE_BF16 ? 1 : 0;
-  hipLaunchKernelGGL((k_route_finish<EPL>), dim3((T + 3) / 4), dim3(256), 0, st, T, E, K, sh.Q, part, logits,
-                     topk_idx, topk_w, out_bf16);
+  if (ds)
+    hipLaunchKernelGGL((k_route_finish_dispatch<EPL>), dim3(1), dim3(256), 0, st, T, E, K, sh.Q, part, logits,
+                       topk_idx, topk_w, out_bf16, ds->group_sizes, ds->offsets, ds->active, ds->sorted_token,
+                       ds->sorted_expert, ds->inv, capacity_of(d));
+  else
+    hipLaunchKernelGGL((k_route_finish<EPL>), dim3((T + 3) / 4), dim3(256), 0, st, T, E, K, sh.Q, part, logits,
+                       topk_idx, topk_w, out_bf16);
 }
 
 hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& r, float* part, float* logits,
-                              int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm) {
+                              int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm,
+                              const DispatchOut* dispatch) {
+  // the dispatch rides along when the finish is a single block
+  const DispatchOut* ds = dispatch && split_router_dispatches(d) ? dispatch : nullptr;
   const SplitShape sh = split_shape(d, r);
   const SliceNorm nm = norm ? *norm : SliceNorm{nullptr, 0, 0.0f, nullptr};
   if (d.act_dtype == KMOE_DTYPE_BF16)
@@ -924,15 +961,15 @@ hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weig
   if (err != hipSuccess) return err;
   const int E = (int)d.num_experts;
   if (E <= 64)
-    launch_finish<1>(d, sh, part, logits, topk_idx, topk_w, st);
+    launch_finish<1>(d, sh, part, logits, topk_idx, topk_w, ds, st);
   else if (E <= 128)
-    launch_finish<2>(d, sh, part, logits, topk_idx, topk_w, st);
+    launch_finish<2>(d, sh, part, logits, topk_idx, topk_w, ds, st);
   else if (E <= 256)
-    launch_finish<4>(d, sh, part, logits, topk_idx, topk_w, st);
+    launch_finish<4>(d, sh, part, logits, topk_idx, topk_w, ds, st);
   else if (E <= 512)
-    launch_finish<8>(d, sh, part, logits, topk_idx, topk_w, st);
+    launch_finish<8>(d, sh, part, logits, topk_idx, topk_w, ds, st);
   else
-    launch_finish<16>(d, sh, part, logits, topk_idx, topk_w, st);
+    launch_finish<16>(d, sh, part, logits, topk_idx, topk_w, ds, st);
   return hipGetLastError();
 }
 
