@@ -904,6 +904,119 @@ __global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* 
 }
 
 
+// ---------------------------------------------------------------------------
+// Decode with at most 8 assignments (T * K <= 8): the down projection and the
+// weighted combine in one kernel, so y never leaves the CU. Block dt owns
+// output columns 16*dt .. 16*dt+15 of every token; waves 2m and 2m+1 compute
+// assignment m = t*K + j (row inv[m] of h_sorted against expert topk_idx[m])
+// as row 0 of a 16-row MFMA tile. The reduction axis keeps the four partial
+// chains of k_down_decode's wave split (chunks [KC*r/4, KC*(r+1)/4)): wave 2m
+// runs chains 0 and 1, wave 2m+1 chains 2 and 3, and the combine adds them in
+// k_down_decode's order, so each y is the value k_down_decode stores; the
+// sum over j then follows k_combine8's order. A wave issues all its weight
+// loads first, its chunks of the h row go through LDS, and the combine's
+// selections and weights are loaded at the start.
+// ---------------------------------------------------------------------------
+template <int KCMAX>
+__global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int D, int I,
+                                                        const uint16_t* __restrict__ h_sorted,
+                                                        const int32_t* __restrict__ topk_idx,
+                                                        const int32_t* __restrict__ inv,
+                                                        const float* __restrict__ topk_w,
+                                                        const int8_t* __restrict__ w2, const float* __restrict__ s2,
+                                                        uint16_t* __restrict__ out, const uint16_t* __restrict__ res) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t hrows[];  // [T*K][I]
+  __shared__ float part[3][kDownCombineMaxRows][16];                // chains 0+1, 2, 3 of row 0
+  const int dt = blockIdx.x, tid = threadIdx.x;
+  const int lane = tid & 63, wv = tid >> 6;  // blockDim.x = 128 * T * K
+  const int m = wv >> 1, half = wv & 1;
+  const int KC = I >> 6;
+  // the combine thread (token tid / 16, column tid % 16) fetches its row of
+  // selections now
+  const bool comb = tid < T * 16;
+  int cinv[kDownCombineMaxRows];
+  float cw[kDownCombineMaxRows];
+#pragma unroll
+  for (int j = 0; j < kDownCombineMaxRows; ++j) {
+    cinv[j] = -1;
+    cw[j] = 0.0f;
+    if (comb && j < K) {
+      cinv[j] = inv[(tid >> 4) * K + j];
+      cw[j] = topk_w[(tid >> 4) * K + j];
+    }
+  }
+  const int p = inv[m];
+  if (p >= 0) {
+    const int e = topk_idx[m];
+    const int cl = (KC * 2 * half) >> 2, ch = (KC * 2 * (half + 1)) >> 2;  // chains 2h and 2h+1
+    const size_t cell = (size_t)(I >> 4) * 256;
+    const int8_t* bp = w2 + ((size_t)e * (D >> 4) + dt) * cell + lane * 16;
+    uint4 q[KCMAX];
+#pragma unroll
+    for (int c = 0; c < KCMAX; ++c)
+      if (cl + c < ch) q[c] = *reinterpret_cast<const uint4*>(bp + (size_t)(cl + c) * 1024);
+    const float sc = s2[(size_t)e * D + dt * 16 + (lane & 15)];
+    // this wave's chunks of the h row (8 pieces of 16 bytes per chunk)
+    uint16_t* hr = hrows + (size_t)m * I;
+    const uint4* src = reinterpret_cast<const uint4*>(h_sorted + (size_t)p * I);
+    for (int i = cl * 8 + lane; i < ch * 8; i += 64) reinterpret_cast<uint4*>(hr)[i] = src[i];
+    // the pieces are read back by other lanes of this wave only
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bool row0 = (lane & 15) == 0;
+    const int koff = 16 * (lane >> 4);
+    floatx4 acc[2];
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = 2 * half + rr;
+      const int c0 = (KC * r) >> 2, c1 = (KC * (r + 1)) >> 2;
+      acc[rr] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < KCMAX; ++c) {
+        if (cl + c >= c0 && cl + c < c1) {
+          uint4 a0 = uint4{0, 0, 0, 0}, a1 = uint4{0, 0, 0, 0};
+          if (row0) {
+            const uint4* ap = reinterpret_cast<const uint4*>(hr + (cl + c) * 64 + koff);
+            a0 = ap[0];
+            a1 = ap[1];
+          }
+          bf16x8 b0, b1;
+          dequant16(q[c], sc, b0, b1);
+          acc[rr] = mfma16(as_bf16x8(a0), b0, acc[rr]);
+          acc[rr] = mfma16(as_bf16x8(a1), b1, acc[rr]);
+        }
+      }
+    }
+    // lanes 0..15 hold row 0, columns 0..15
+    if (lane < 16) {
+      if (half == 0) {
+        part[0][m][lane] = acc[0][0] + acc[1][0];
+      } else {
+        part[1][m][lane] = acc[0][0];
+        part[2][m][lane] = acc[1][0];
+      }
+    }
+  }
+  __syncthreads();
+  if (comb) {
+    const int t = tid >> 4, col = tid & 15;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kDownCombineMaxRows; ++j) {
+      // a dropped assignment (inv < 0, fixed_capacity) adds nothing
+      if (j < K && cinv[j] >= 0) {
+        const int mj = t * K + j;
+        const float y = round_bf16((part[0][mj][col] + part[1][mj][col]) + part[2][mj][col]);
+        acc = __builtin_fmaf(cw[j], y, acc);
+      }
+    }
+    const int64_t o = (int64_t)t * D + dt * 16 + col;
+    if (res) acc = bf16_bits_to_f32(res[o]) + round_bf16(acc);
+    out[o] = f32_to_bf16_bits(acc);
+  }
+}
+
 template <typename A>
 __global__ __launch_bounds__(256) void k_cast_from_f32(int64_t n, const float* __restrict__ in, A* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1062,6 +1175,34 @@ hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_
       hipLaunchKernelGGL((k_combine1<float>), grid, dim3(256), 0, st, T, K, D, reinterpret_cast<const float*>(y_sorted),
                          inv, topk_w, reinterpret_cast<float*>(out), reinterpret_cast<const float*>(res));
   }
+  return hipGetLastError();
+}
+
+// the weights of a wave's chunks (half the reduction) stay in registers: at
+// most 12 chunks of 64
+bool down_combine_fits(const kmoe_desc& d) {
+  const int64_t M = d.tokens * d.top_k, KC = d.intermediate / 64;
+  return M >= 1 && M <= kDownCombineMaxRows && KC <= 24 && M * d.intermediate * 2 <= 65536;
+}
+
+hipError_t launch_down_combine(const kmoe_desc& d, const void* h_sorted, const int32_t* topk_idx, const int32_t* inv,
+                               const float* topk_w, const kmoe_packed_experts& p, void* out, hipStream_t st,
+                               const void* res) {
+  const int T = (int)d.tokens, K = (int)d.top_k, D = (int)d.hidden, I = (int)d.intermediate;
+  if (!down_combine_fits(d)) return hipErrorInvalidValue;
+  const dim3 grid(D / 16), block(128 * T * K);
+  const size_t lds = (size_t)T * K * I * 2;
+  const uint16_t* hb = reinterpret_cast<const uint16_t*>(h_sorted);
+  const int8_t* w2 = reinterpret_cast<const int8_t*>(p.w2);
+  const float* s2 = reinterpret_cast<const float*>(p.s2);
+  uint16_t* ob = reinterpret_cast<uint16_t*>(out);
+  const uint16_t* rb = reinterpret_cast<const uint16_t*>(res);
+  if (I / 64 <= 12)
+    hipLaunchKernelGGL((k_down_combine<6>), grid, block, lds, st, T, K, D, I, hb, topk_idx, inv, topk_w, w2, s2, ob,
+                       rb);
+  else
+    hipLaunchKernelGGL((k_down_combine<12>), grid, block, lds, st, T, K, D, I, hb, topk_idx, inv, topk_w, w2, s2, ob,
+                       rb);
   return hipGetLastError();
 }
 

@@ -22,8 +22,9 @@ struct SliceNorm {
   void* h2;  // [T][D] normalised rows (activation dtype)
 };
 // The dispatch sort's outputs (as launch_dispatch). Given to the split router,
-// it runs the sort itself when the tokens fit one finish block (T <= 4;
-// split_router_dispatches(d)), and the caller skips launch_dispatch.
+// it runs the sort itself when the finish is a single block of one wave per
+// token (T <= 16; split_router_dispatches(d)), and the caller skips
+// launch_dispatch.
 struct DispatchOut {
   int32_t* group_sizes;
   int32_t* offsets;
@@ -32,7 +33,7 @@ struct DispatchOut {
   int32_t* sorted_expert;
   int32_t* inv;
 };
-inline bool split_router_dispatches(const kmoe_desc& d) { return d.tokens <= 4; }
+inline bool split_router_dispatches(const kmoe_desc& d) { return d.tokens <= 16; }
 size_t route_split_part_floats(const kmoe_desc& d);
 hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part, float* logits,
                               int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm = nullptr,
@@ -56,6 +57,13 @@ hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, 
 // out = round(sum_j w * y_sorted[inv]) [+ residual res, rounded again], res may be NULL
 hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
                           hipStream_t st, const void* res = nullptr);
+// Packed decode with T * K <= 8 (down_combine_fits): the down projection and
+// the combine (with residual res, may be NULL) in one kernel; out is
+// bit-identical to the packed decode down kernel followed by launch_combine.
+bool down_combine_fits(const kmoe_desc& d);
+hipError_t launch_down_combine(const kmoe_desc& d, const void* h_sorted, const int32_t* topk_idx, const int32_t* inv,
+                               const float* topk_w, const kmoe_packed_experts& p, void* out, hipStream_t st,
+                               const void* res);
 hipError_t launch_topk_w_cast(const kmoe_desc& d, const float* topk_w, void* out, hipStream_t st);
 
 // block.hip

@@ -508,14 +508,15 @@ __device__ __forceinline__ void finish_token(int t, int E, int K, int Q, const f
                                              float* __restrict__ topk_w, int out_bf16, int32_t* idx_lds,
                                              TopkLds& tk) {
   const int lane = threadIdx.x & 63;
+  const float* const pt = part + (int64_t)t * Q * E;  // [Q][E] partials of token t
   float v[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int e = lane + 64 * i;
     float p[kMaxRouterSlices / 4];
+    const float* pq = pt + e;
 #pragma unroll
-    for (int q = 0; q < kMaxRouterSlices / 4; ++q)
-      p[q] = (q < Q && e < E) ? part[((int64_t)t * Q + q) * E + e] : 0.0f;
+    for (int q = 0; q < kMaxRouterSlices / 4; ++q, pq += E) p[q] = (q < Q && e < E) ? *pq : 0.0f;
 #pragma unroll
     for (int st = 1; st < kMaxRouterSlices / 4; st <<= 1)
       if (st < Q)
@@ -719,17 +720,20 @@ __device__ void dispatch_chunk(int T, int E, int K, int b, int nblk, const int32
   }
 }
 
-// T <= 4: the finish is one block, so it also runs the dispatch sort of its
-// tokens (the selections pass through LDS; no second kernel).
-template <int EPL>
-__global__ __launch_bounds__(256) void k_route_finish_dispatch(
+// T <= NW <= 16: the finish is one block of NW waves, one token each, so it
+// also runs the dispatch sort of the tokens (the selections pass through LDS;
+// no second kernel). At larger T a single block's serial top-ks and sort
+// cost more than the separate dispatch kernel.
+template <int EPL, int NW>
+__global__ __launch_bounds__(64 * NW) void k_route_finish_dispatch(
     int T, int E, int K, int Q, const float* __restrict__ part, float* __restrict__ logits,
     int32_t* __restrict__ topk_idx, float* __restrict__ topk_w, int out_bf16, int32_t* __restrict__ group_sizes,
     int32_t* __restrict__ offsets, int32_t* __restrict__ active, int32_t* __restrict__ sorted_token,
     int32_t* __restrict__ sorted_expert, int32_t* __restrict__ inv, int cap) {
-  __shared__ TopkLds tk[4];
+  static_assert(NW >= 4 && NW <= 16, "dispatch_chunk needs 256 threads; one wave per token");
+  __shared__ TopkLds tk[NW];
   __shared__ DispatchLds L;
-  __shared__ int32_t idx_lds[4 * kMaxTopK];
+  __shared__ int32_t idx_lds[NW * kMaxTopK];
   const int w = threadIdx.x >> 6;
   if (w < T) finish_token<EPL>(w, E, K, Q, part, logits, topk_idx, topk_w, out_bf16, idx_lds, tk[w]);
   __syncthreads();
@@ -937,8 +941,12 @@ static void launch_finish(const kmoe_desc& d, const SplitShape& sh, const float*
                           int32_t* topk_idx, float* topk_w, const DispatchOut* ds, hipStream_t st) {
   const int T = (int)d.tokens, E = (int)d.num_experts, K = (int)d.top_k;
   const int out_bf16 = d.act_dtype == KMOE_DTYPE_BF16 ? 1 : 0;
-  if (ds)
-    hipLaunchKernelGGL((k_route_finish_dispatch<EPL>), dim3(1), dim3(256), 0, st, T, E, K, sh.Q, part, logits,
+  if (ds && T <= 4)
+    hipLaunchKernelGGL((k_route_finish_dispatch<EPL, 4>), dim3(1), dim3(256), 0, st, T, E, K, sh.Q, part, logits,
+                       topk_idx, topk_w, out_bf16, ds->group_sizes, ds->offsets, ds->active, ds->sorted_token,
+                       ds->sorted_expert, ds->inv, capacity_of(d));
+  else if (ds)
+    hipLaunchKernelGGL((k_route_finish_dispatch<EPL, 16>), dim3(1), dim3(1024), 0, st, T, E, K, sh.Q, part, logits,
                        topk_idx, topk_w, out_bf16, ds->group_sizes, ds->offsets, ds->active, ds->sorted_token,
                        ds->sorted_expert, ds->inv, capacity_of(d));
   else

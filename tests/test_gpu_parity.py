@@ -206,9 +206,22 @@ def test_30b_skewed_routing(dev, l30):
 
 
 def test_235b_layer(dev):
+    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+
     layer = make_layer("235b", seed=1)
     _prefill_sampled(layer, 16, seed=16, n_tok=16)
     _prefill_sampled(layer, 2048, seed=2048, n_tok=24)
+    # T = 1 and 2: the whole layer (fused down + combine at T = 1, each wave
+    # holding 12 of the 24 chunks of the reduction) against the staged calls
+    cfg = moe_layer_config(hidden=layer.D, experts=layer.E, top_k=layer.K, intermediate=layer.I)
+    for T in (1, 2):
+        _prefill_sampled(layer, T, seed=T, n_tok=T)
+        x = make_x(T, layer.D, seed=T)
+        r, d = _route_and_dispatch(x, layer.router, layer.E, layer.K)
+        h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K)
+        staged = moe_stages.combine(y, d["inv"], r["w"], k=layer.K)
+        out = moe_swiglu_ffn(x.reshape(1, T, layer.D), layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
+        assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
     del layer
     torch.cuda.empty_cache()
 
@@ -254,6 +267,32 @@ def test_whole_block_matches_staged_path(dev, l30, T):
             assert torch.equal(idx, r["idx"])
             assert torch.equal(w.float(), r["w"])
             assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
+
+
+@pytest.mark.parametrize("T,K", [(1, 8), (2, 4), (2, 8), (3, 8), (8, 8)])
+def test_whole_block_with_drops_matches_staged_path(dev, l30, T, K):
+    """Capacity 1 under a skewed router drops assignments whenever two tokens
+    pick one expert; at T * K <= 8 the whole-block call runs the down
+    projection and the combine as one kernel, which must skip the dropped rows
+    exactly as the staged combine does and give the staged output bit for
+    bit."""
+    from kappa_amd.qwen3 import moe_stages
+    from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _moe_forward
+
+    router = skew_router(l30.router, lam=1.5)
+    x = make_x(T, l30.D, seed=760 + T)
+    x[:, 0] = 1.0
+    r = moe_stages.route(x, router, num_experts=l30.E, k=K)
+    d = moe_stages.dispatch(r["idx"], r["hist"], num_experts=l30.E, capacity=1)
+    if T > 1:
+        assert bool((d["inv"] < 0).any())
+    h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=K, capacity=1)
+    staged = moe_stages.combine(y, d["inv"], r["w"], k=K)
+    out = _moe_forward(
+        x.reshape(1, T, l30.D), router, l30.gate, l30.up, l30.down, num_experts=l30.E, num_experts_per_tok=K,
+        decode_threshold=64, packed=PACK_CACHE.get(l30.gate, l30.up, l30.down), capacity=1,
+    )  # fmt: skip
+    assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
 
 
 def test_layout_native_experts_match_packed(dev, l30):
