@@ -102,7 +102,7 @@ __device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode (T <= 64): one block per (active expert, 16-column group); the four
+// Decode (T <= 64): one block per (active expert, 16-column group); the WPB
 // waves split the reduction axis and are summed in wave order through LDS.
 // Each weight byte is read exactly once per call. A wave issues the weight
 // loads of a batch of NB 64-deep chunks (NB x 1 KB per operand in flight)
@@ -110,26 +110,51 @@ __device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
 // and loads the activation fragments, dequantises and runs the MFMAs; the raw
 // int8 stays in registers across 16-row blocks. GUARD handles a chunk count
 // per wave that NB does not divide.
+//
+// DENSE (T <= 16, one batch per wave): the 16-row tile is the T tokens
+// themselves, in token order, instead of the expert's gathered rows; it pays
+// while T is small, since every block reads all T activation rows. A row's
+// products do not depend on the other rows of the tile, so each stored row is
+// the value the gathered tile gives; only the rows of the tokens routed to
+// the expert are stored. The activation loads then depend on nothing and are
+// issued first, ahead of the expert lookup.
 // ---------------------------------------------------------------------------
-template <int WPB, int NB, bool GUARD>
-__global__ __launch_bounds__(512) void k_gateup_decode(int D, int I, int E, const uint16_t* __restrict__ x,
+template <int WPB, int NB, bool GUARD, int MRB, bool DENSE>
+__global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int E, const uint16_t* __restrict__ x,
                                                         const int32_t* __restrict__ offsets,
                                                         const int32_t* __restrict__ active,
                                                         const int32_t* __restrict__ sorted_token,
                                                         const int8_t* __restrict__ w13, const float* __restrict__ s13,
                                                         uint16_t* __restrict__ h_sorted, int cap) {
-  __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][kDecodeMaxRowBlocks][2][64];
+  static_assert(!DENSE || (MRB == 1 && !GUARD), "dense tiles: one row block, one batch per wave");
+  __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][MRB][2][64];
+  __shared__ int srt[16];  // DENSE: the tokens of the expert's rows
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int IG = I >> 4, KC = D >> 6;
+  const int c0 = (KC * wv) / WPB, c1 = (KC * (wv + 1)) / WPB;
+  const int koff = 16 * (lane >> 4);
+  uint4 da0[DENSE ? NB : 1], da1[DENSE ? NB : 1];
+  if (DENSE) {
+    const int t = lane & 15;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      da0[i] = uint4{0, 0, 0, 0};
+      da1[i] = uint4{0, 0, 0, 0};
+      if (t < T) {
+        const uint4* ap = reinterpret_cast<const uint4*>(x + (size_t)t * D + koff + (c0 + i) * 64);
+        da0[i] = ap[0];
+        da1[i] = ap[1];
+      }
+    }
+  }
   const int ig = blockIdx.x;
   const int slot = blockIdx.y;
   const int n_active = active[E];
   const int e = active[slot < E ? slot : 0];
   if (slot >= n_active) return;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int IG = I >> 4, KC = D >> 6;
   const size_t cell = (size_t)(D >> 4) * 256;
   const int8_t* bg = w13 + (((size_t)e * IG + ig) * 2 + 0) * cell + lane * 16;
   const int8_t* bu = bg + cell;
-  const int c0 = (KC * wv) / WPB, c1 = (KC * (wv + 1)) / WPB;
   uint4 qg[NB], qu[NB];
   auto load_w = [&](int cb) {
 #pragma unroll
@@ -145,29 +170,36 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int D, int I, int E, cons
   const float su = s13[(((size_t)e * IG + ig) * 2 + 1) * 16 + (lane & 15)];
   const int r0 = offsets[e];
   const int nrows = min(offsets[e + 1] - r0, cap);
-  const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
-  const int koff = 16 * (lane >> 4);
-  const uint16_t* xr[kDecodeMaxRowBlocks];
+  const int nrb = DENSE ? 1 : min((nrows + 15) >> 4, MRB);
+  if (DENSE && wv == 0 && lane < nrows) srt[lane] = sorted_token[r0 + lane];
+  const uint16_t* xr[MRB];
+  if (!DENSE) {
 #pragma unroll
-  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
-    const int row = rb * 16 + (lane & 15);
-    const int tok = sorted_token[r0 + min(row, nrows - 1)];
-    xr[rb] = row < nrows ? x + (size_t)tok * D + koff : nullptr;
+    for (int rb = 0; rb < MRB; ++rb) {
+      const int row = rb * 16 + (lane & 15);
+      const int tok = sorted_token[r0 + min(row, nrows - 1)];
+      xr[rb] = row < nrows ? x + (size_t)tok * D + koff : nullptr;
+    }
   }
-  floatx4 ag[kDecodeMaxRowBlocks], au[kDecodeMaxRowBlocks];
+  floatx4 ag[MRB], au[MRB];
 #pragma unroll
-  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+  for (int rb = 0; rb < MRB; ++rb) {
     ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
     au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
   for (int cb = c0; cb < c1; cb += NB) {
     if (cb != c0) load_w(cb);
 #pragma unroll
-    for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+    for (int rb = 0; rb < MRB; ++rb) {
       if (rb < nrb) {
         uint4 a0[NB], a1[NB];
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
+          if (DENSE) {
+            a0[i] = da0[i];
+            a1[i] = da1[i];
+            continue;
+          }
           a0[i] = uint4{0, 0, 0, 0};
           a1[i] = uint4{0, 0, 0, 0};
           if (xr[rb] && (!GUARD || cb + i < c1)) {
@@ -193,7 +225,7 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int D, int I, int E, cons
   }
   if (wv > 0) {
 #pragma unroll
-    for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+    for (int rb = 0; rb < MRB; ++rb) {
       if (rb < nrb) {
         red[wv - 1][rb][0][lane] = ag[rb];
         red[wv - 1][rb][1][lane] = au[rb];
@@ -203,7 +235,7 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int D, int I, int E, cons
   __syncthreads();
   if (wv != 0) return;
 #pragma unroll
-  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+  for (int rb = 0; rb < MRB; ++rb) {
     if (rb >= nrb) break;
     floatx4 g = ag[rb], u = au[rb];
 #pragma unroll
@@ -214,9 +246,16 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int D, int I, int E, cons
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int row = rb * 16 + 4 * (lane >> 4) + j;
-      if (row < nrows) {
+      // DENSE: tile row = token; find its position among the expert's rows
+      int pos = row < nrows ? r0 + row : -1;
+      if (DENSE) {
+        pos = -1;
+        for (int r = 0; r < nrows; ++r)
+          if (srt[r] == row) pos = r0 + r;
+      }
+      if (pos >= 0) {
         const float gv = round_bf16(g[j]), uv = round_bf16(u[j]);
-        h_sorted[(size_t)(r0 + row) * I + ig * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(gv) * uv);
+        h_sorted[(size_t)pos * I + ig * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(gv) * uv);
       }
     }
   }
@@ -1048,14 +1087,32 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
     // shapes from a sweep on MI355X (30B-A3B layer, T = 1..64): four waves split
     // the reduction, batches of 4 (gate/up) or 3 (down) chunks per load stage
     if (stages & kStageGateUp) {
-      const int cpw = (D / 64) / 4;  // chunks per wave
       const dim3 grid(I / 16, slots);
-      if ((D / 64) % 4 == 0 && cpw % 4 == 0)
-        hipLaunchKernelGGL((k_gateup_decode<4, 4, false>), grid, dim3(256), 0, st, D, I, E, xb, offsets, active,
-                           sorted_token, w13, s13, hb, cap);
-      else
-        hipLaunchKernelGGL((k_gateup_decode<4, 4, true>), grid, dim3(256), 0, st, D, I, E, xb, offsets, active,
-                           sorted_token, w13, s13, hb, cap);
+      if (T <= 16 && (D / 64 == 32 || D / 64 == 64)) {
+        // at most one 16-row block per expert: eight waves of one load batch
+        // each (4 chunks at D = 2048, 8 at D = 4096), every load of a wave in
+        // flight at once. Up to T = 4 the tile is the T tokens themselves
+        // (DENSE); beyond, gathering only the expert's rows reads less.
+        const bool dense = T <= 4;
+        if (D / 64 == 32 && dense)
+          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, true>), grid, dim3(512), 0, st, T, D, I, E, xb, offsets,
+                             active, sorted_token, w13, s13, hb, cap);
+        else if (D / 64 == 32)
+          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, false>), grid, dim3(512), 0, st, T, D, I, E, xb,
+                             offsets, active, sorted_token, w13, s13, hb, cap);
+        else if (dense)
+          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, true>), grid, dim3(512), 0, st, T, D, I, E, xb, offsets,
+                             active, sorted_token, w13, s13, hb, cap);
+        else
+          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, false>), grid, dim3(512), 0, st, T, D, I, E, xb,
+                             offsets, active, sorted_token, w13, s13, hb, cap);
+      } else if ((D / 64) % 16 == 0) {
+        hipLaunchKernelGGL((k_gateup_decode<4, 4, false, kDecodeMaxRowBlocks, false>), grid, dim3(256), 0, st, T, D,
+                           I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
+      } else {
+        hipLaunchKernelGGL((k_gateup_decode<4, 4, true, kDecodeMaxRowBlocks, false>), grid, dim3(256), 0, st, T, D, I,
+                           E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
+      }
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
     }

@@ -295,6 +295,25 @@ def test_whole_block_with_drops_matches_staged_path(dev, l30, T, K):
     assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
 
 
+@pytest.mark.parametrize("T", [1, 4, 8, 15, 63])
+def test_decode_batch_invariance(dev, l30, T):
+    """A token's output does not depend on the other tokens of the call: the
+    first T rows of a (T + 1)-token call equal the T-token call bit for bit.
+    The pairs cross the kernel-shape switches of the decode path that keep the
+    summation order (fused down + combine up to T * K = 8, the dense token
+    tile of the gate/up kernel up to T = 4, the one-block finish + dispatch up
+    to T = 4 and T = 16). Between T = 16 and 17 the
+    gate/up reduction goes from eight wave chains to four, a different
+    grouping of the same sum, so that pair is not bit-identical."""
+    from kappa_amd.qwen3 import moe_layer_config, moe_swiglu_ffn
+
+    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
+    x = make_x(T + 1, l30.D, seed=880 + T)
+    a = moe_swiglu_ffn(x[:T].reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
+    b = moe_swiglu_ffn(x.reshape(1, T + 1, l30.D), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
+    assert torch.equal(a.reshape(T, l30.D), b.reshape(T + 1, l30.D)[:T])
+
+
 def test_layout_native_experts_match_packed(dev, l30):
     from kappa_amd.qwen3 import moe_stages
 
