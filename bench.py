@@ -15,7 +15,8 @@ Prints ONE JSON line on stdout (logs go to stderr):
   roofline     the dominant decode kernel (gate/up + SwiGLU), HBM-bound:
                algorithmic bytes per launch / mean launch time from HIP events
   prefill      the 4096-token prefill chunk: tokens/s and the MFMA roofline
-               of its dominant kernel (the gate/up grouped GEMM)
+               of its dominant kernel (the gate/up grouped GEMM), next to
+               hipBLASLt bf16 GEMMs of the same shapes (library_reference)
   cpu_baseline the oracle (the C restatement of the reference algorithm),
                OpenMP on this host's cores, on a bounded sample
 """
@@ -218,6 +219,40 @@ def measured_traffic(kernel: str, workload: str):
     except OSError:
         pass
     return None
+
+
+def library_reference(T, D, I, E, K, reps=20):
+    """hipBLASLt (torch.bmm / torch.mm, bf16) on the prefill expert shapes with
+    uniform routing, M = T*K/E rows per expert, bf16 weights (no int8
+    dequantisation, no gather, no SwiGLU): a vendor-library reference point
+    for the grouped GEMMs, not part of the block."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    M = T * K // E
+    out = {}
+    for name, (bs, m, k, n) in (
+        ("gate_up_bmm", (E, M, D, 2 * I)),
+        ("down_bmm", (E, M, I, D)),
+        ("gate_up_one_gemm", (1, T * K, D, 2 * I)),
+    ):
+        a = torch.randn(bs, m, k, device=dev).to(torch.bfloat16)
+        b = torch.randn(bs, k, n, device=dev).to(torch.bfloat16).contiguous()
+        for _ in range(3):
+            torch.bmm(a, b)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            torch.bmm(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        tf = 2.0 * bs * m * k * n / (us * 1e-6) / 1e12
+        out[name] = {"shape": [bs, m, k, n], "us": us, "tflops": tf, "frac": tf / BF16_PEAK_TFLOPS}
+        del a, b
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(layer, T, budget_s=12.0, max_reps=20):
@@ -447,6 +482,7 @@ def main():
                 "mean_launch_us": gms * 1e3,
             },
         }
+        result["prefill"]["library_reference"] = library_reference(Tp, D, I, E, K)
         log(f"bench: prefill {result['prefill']}")
 
     if not args.no_cpu_baseline:
