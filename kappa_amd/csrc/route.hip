@@ -248,27 +248,44 @@ __global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int 
       const int d1 = min(D, d0 + kRouterSlice);
       const float* xs = lds + s * XP - d0 * TB;
       if (vec && d1 - d0 == kRouterSlice) {
-        typename Row::Raw cur[U], nxt[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) Row::load(rw, (int64_t)(d0 + u) * E + e0, nxt[u]);
-        for (int db = d0; db < d1; db += U) {
-#pragma unroll
-          for (int u = 0; u < U; ++u) cur[u] = nxt[u];
-          if (db + U < d1) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) Row::load(rw, (int64_t)(db + U + u) * E + e0, nxt[u]);
-          }
+        // two register stages used in turn (the loop body covers 2U rows, and
+        // 2U divides the 64 rows of a slice), so no stage is copied
+        static_assert(kRouterSlice % (2 * U) == 0, "two stages per step");
+        typename Row::Raw b0[U], b1[U];
+        auto rows = [&](const typename Row::Raw* raw, int db) {
 #pragma unroll
           for (int u = 0; u < U; ++u) {
             float r[EPL], xv[TB];
-            Row::convert(cur[u], sc, r);
+            Row::convert(raw[u], sc, r);
+            // the x stage is 16-byte aligned for TB >= 4 (slice stride
+            // 64*TB + 4 floats, row stride TB floats)
+            if constexpr (TB % 4 == 0) {
 #pragma unroll
-            for (int tt = 0; tt < TB; ++tt) xv[tt] = xs[(db + u) * TB + tt];
+              for (int q = 0; q < TB / 4; ++q) {
+                const float4 v4 = *reinterpret_cast<const float4*>(xs + (db + u) * TB + 4 * q);
+                xv[4 * q] = v4.x, xv[4 * q + 1] = v4.y, xv[4 * q + 2] = v4.z, xv[4 * q + 3] = v4.w;
+              }
+            } else {
+#pragma unroll
+              for (int tt = 0; tt < TB; ++tt) xv[tt] = xs[(db + u) * TB + tt];
+            }
 #pragma unroll
             for (int tt = 0; tt < TB; ++tt)
 #pragma unroll
               for (int i = 0; i < EPL; ++i) c.v[tt][i] = __builtin_fmaf(xv[tt], r[i], c.v[tt][i]);
           }
+        };
+#pragma unroll
+        for (int u = 0; u < U; ++u) Row::load(rw, (int64_t)(d0 + u) * E + e0, b0[u]);
+        for (int db = d0; db < d1; db += 2 * U) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) Row::load(rw, (int64_t)(db + U + u) * E + e0, b1[u]);
+          rows(b0, db);
+          if (db + 2 * U < d1) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) Row::load(rw, (int64_t)(db + 2 * U + u) * E + e0, b0[u]);
+          }
+          rows(b1, db + U);
         }
       } else {
         for (int d = d0; d < d1; ++d) {
