@@ -44,6 +44,15 @@ __device__ __forceinline__ void dequant16(const uint4 q, const float s, bf16x8& 
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// 16 bytes with a nontemporal load: for weights a decode kernel reads exactly
+// once (streaming reads this way sustain ~7.1 TB/s on MI355X against ~6.3 TB/s
+// for ordinary loads, which also allocate in the caches)
+__device__ __forceinline__ uint4 load_stream16(const int8_t* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+}
+
 __device__ __forceinline__ floatx4 mfma16(const bf16x8 a, const bf16x8 b, const floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -160,8 +169,8 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       if (!GUARD || cb + i < c1) {
-        qg[i] = *reinterpret_cast<const uint4*>(bg + (size_t)(cb + i) * 1024);
-        qu[i] = *reinterpret_cast<const uint4*>(bu + (size_t)(cb + i) * 1024);
+        qg[i] = load_stream16(bg + (size_t)(cb + i) * 1024);
+        qu[i] = load_stream16(bu + (size_t)(cb + i) * 1024);
       }
     }
   };
@@ -287,7 +296,7 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
     for (int i = 0; i < NB; ++i)
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg)
-        if (!GUARD || cb + i < c1) q[i][cg] = *reinterpret_cast<const uint4*>(bp + cg * cell + (size_t)(cb + i) * 1024);
+        if (!GUARD || cb + i < c1) q[i][cg] = load_stream16(bp + cg * cell + (size_t)(cb + i) * 1024);
   };
   load_w(c0);
   float sc[NCG];
@@ -993,7 +1002,7 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int D, int 
     uint4 q[KCMAX];
 #pragma unroll
     for (int c = 0; c < KCMAX; ++c)
-      if (cl + c < ch) q[c] = *reinterpret_cast<const uint4*>(bp + (size_t)(cl + c) * 1024);
+      if (cl + c < ch) q[c] = load_stream16(bp + (size_t)(cl + c) * 1024);
     const float sc = s2[(size_t)e * D + dt * 16 + (lane & 15)];
     // this wave's chunks of the h row (8 pieces of 16 bytes per chunk)
     uint16_t* hr = hrows + (size_t)m * I;
