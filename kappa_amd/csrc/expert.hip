@@ -44,9 +44,9 @@ __device__ __forceinline__ void dequant16(const uint4 q, const float s, bf16x8& 
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// 16 bytes with a nontemporal load: for weights a decode kernel reads exactly
-// once (streaming reads this way sustain ~7.1 TB/s on MI355X against ~6.3 TB/s
-// for ordinary loads, which also allocate in the caches)
+// 16 bytes with a nontemporal load: for data a kernel reads exactly once, such
+// as the decode weights (streaming reads this way sustain ~7.1 TB/s on MI355X
+// against ~6.3 TB/s for ordinary loads, which also allocate in the caches)
 __device__ __forceinline__ uint4 load_stream16(const int8_t* p) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -865,8 +865,9 @@ template <typename A>
 struct Vec8;
 template <>
 struct Vec8<uint16_t> {
+  // the combine reads each y row and residual once: nontemporal loads
   __device__ __forceinline__ static void load(const uint16_t* p, float* v) {
-    const uint4 q = *reinterpret_cast<const uint4*>(p);
+    const uint4 q = load_stream16(reinterpret_cast<const int8_t*>(p));
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -885,8 +886,11 @@ struct Vec8<uint16_t> {
 template <>
 struct Vec8<float> {
   __device__ __forceinline__ static void load(const float* p, float* v) {
-    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
-    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    const uint4 a = load_stream16(reinterpret_cast<const int8_t*>(p));
+    const uint4 b = load_stream16(reinterpret_cast<const int8_t*>(p + 4));
+    v[0] = __uint_as_float(a.x), v[1] = __uint_as_float(a.y), v[2] = __uint_as_float(a.z);
+    v[3] = __uint_as_float(a.w), v[4] = __uint_as_float(b.x), v[5] = __uint_as_float(b.y);
+    v[6] = __uint_as_float(b.z), v[7] = __uint_as_float(b.w);
   }
   __device__ __forceinline__ static void store(float* p, const float* v) {
     reinterpret_cast<float4*>(p)[0] = float4{v[0], v[1], v[2], v[3]};
