@@ -295,6 +295,27 @@ def test_whole_block_with_drops_matches_staged_path(dev, l30, T, K):
     assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
 
 
+@pytest.mark.parametrize("T,K", [(1, 1), (1, 8), (3, 2), (4, 2), (8, 1), (2, 3)])
+def test_fused_down_combine_shapes(dev, l30, T, K):
+    """The whole-block call at T * K <= 8 (down projection and combine in one
+    kernel, two waves per assignment, T * 16 combine threads) against the
+    staged calls, bit for bit, over the token/top-k splits of eight
+    assignments and fewer."""
+    from kappa_amd.qwen3 import moe_stages
+    from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _moe_forward
+
+    x = make_x(T, l30.D, seed=830 + 10 * T + K)
+    r = moe_stages.route(x, l30.router, num_experts=l30.E, k=K)
+    d = moe_stages.dispatch(r["idx"], r["hist"], num_experts=l30.E)
+    h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=K)
+    staged = moe_stages.combine(y, d["inv"], r["w"], k=K)
+    out = _moe_forward(
+        x.reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, num_experts=l30.E, num_experts_per_tok=K,
+        decode_threshold=64, packed=PACK_CACHE.get(l30.gate, l30.up, l30.down),
+    )  # fmt: skip
+    assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
+
+
 @pytest.mark.parametrize("T", [1, 4, 8, 15, 63])
 def test_decode_batch_invariance(dev, l30, T):
     """A token's output does not depend on the other tokens of the call: the
