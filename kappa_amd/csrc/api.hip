@@ -367,7 +367,7 @@ kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host
     KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, hist, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
   }
   if (packed_ok(*desc, packed) && decode_path(*desc) && kmoe_host::down_combine_fits(*desc)) {
-    // at most 8 assignments: the down projection and the combine in one kernel
+    // at most 32 assignments: the down projection and the combine in one kernel
     KMOE_TRY(expert_stage(*desc, kmoe_host::kStageGateUp, xin, off, act, stok, sexp, gate, up, down, packed, hs, ys,
                           st));
     KMOE_HIP(kmoe_host::launch_down_combine(*desc, hs, tidx, inv, tw, *packed, out, st, res), "down+combine kernel");

@@ -20,7 +20,8 @@ constexpr int kMaxTopK = 64;
 constexpr int kMaxRouterSlices = 64;  // D <= 4096
 // Decode kernels keep up to this many 16-row blocks of one expert in registers.
 constexpr int kDecodeMaxRowBlocks = 4;  // T <= 64 tokens
-constexpr int kDownCombineMaxRows = 8;  // assignments (T * K) of the fused decode down + combine
+constexpr int kDownCombineMaxRows = 8;          // assignments per block of the fused decode down + combine
+constexpr int kDownCombineMaxAssignments = 32;  // T * K it takes
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));

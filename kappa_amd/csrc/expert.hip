@@ -11,6 +11,8 @@
 // inside a 64-wide chunk is permuted: lane l supplies k = 16*(l/16) + 8*s + 0..7
 // in sub-step s, for both operands, which matches the packed layout
 // [.., k/16, col, 16 k] where each lane's 16 bytes are one column's 16 k.
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 
@@ -957,35 +959,40 @@ __global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* 
 
 
 // ---------------------------------------------------------------------------
-// Decode with at most 8 assignments (T * K <= 8): the down projection and the
-// weighted combine in one kernel, so y never leaves the CU. Block dt owns
-// output columns 16*dt .. 16*dt+15 of every token; waves 2m and 2m+1 compute
-// assignment m = t*K + j (row inv[m] of h_sorted against expert topk_idx[m])
-// as row 0 of a 16-row MFMA tile. The reduction axis keeps the four partial
-// chains of k_down_decode's wave split (chunks [KC*r/4, KC*(r+1)/4)): wave 2m
-// runs chains 0 and 1, wave 2m+1 chains 2 and 3, and the combine adds them in
+// Decode with few assignments (T * K <= 32, K <= 8): the down projection and
+// the weighted combine in one kernel, so y never leaves the CU. Block
+// (dt, tb) owns output columns 16*dt .. 16*dt+15 of the TPB = 8 / K tokens
+// tb*TPB ...; waves 2m and 2m+1 compute the block's assignment m (row inv of
+// h_sorted against expert topk_idx, global index tb*TPB*K + m) as row 0 of a
+// 16-row MFMA tile. The reduction axis keeps the four partial chains of
+// k_down_decode's wave split (chunks [KC*r/4, KC*(r+1)/4)): wave 2m runs
+// chains 0 and 1, wave 2m+1 chains 2 and 3, and the combine adds them in
 // k_down_decode's order, so each y is the value k_down_decode stores; the
 // sum over j then follows k_combine8's order. A wave issues all its weight
 // loads first, its chunks of the h row go through LDS, and the combine's
-// selections and weights are loaded at the start.
+// selections and weights are loaded at the start. An expert picked by tokens
+// of several blocks is read by each of them, which is why the fused form stops
+// at 32 assignments (at 64 it was slower than the two kernels).
 // ---------------------------------------------------------------------------
 template <int KCMAX>
-__global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int D, int I,
+__global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, int D, int I,
                                                         const uint16_t* __restrict__ h_sorted,
                                                         const int32_t* __restrict__ topk_idx,
                                                         const int32_t* __restrict__ inv,
                                                         const float* __restrict__ topk_w,
                                                         const int8_t* __restrict__ w2, const float* __restrict__ s2,
                                                         uint16_t* __restrict__ out, const uint16_t* __restrict__ res) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t hrows[];  // [T*K][I]
+  extern __shared__ __attribute__((aligned(16))) uint16_t hrows[];  // [TPB*K][I]
   __shared__ float part[3][kDownCombineMaxRows][16];                // chains 0+1, 2, 3 of row 0
   const int dt = blockIdx.x, tid = threadIdx.x;
-  const int lane = tid & 63, wv = tid >> 6;  // blockDim.x = 128 * T * K
+  const int lane = tid & 63, wv = tid >> 6;  // blockDim.x = 128 * TPB * K
   const int m = wv >> 1, half = wv & 1;
+  const int t0 = blockIdx.y * TPB, nt = min(TPB, T - t0);  // this block's tokens
+  const int64_t a0 = (int64_t)t0 * K;                      // its first assignment
   const int KC = I >> 6;
-  // the combine thread (token tid / 16, column tid % 16) fetches its row of
-  // selections now
-  const bool comb = tid < T * 16;
+  // the combine thread (token t0 + tid / 16, column tid % 16) fetches its row
+  // of selections now
+  const bool comb = tid < nt * 16;
   int cinv[kDownCombineMaxRows];
   float cw[kDownCombineMaxRows];
 #pragma unroll
@@ -993,13 +1000,13 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int D, int 
     cinv[j] = -1;
     cw[j] = 0.0f;
     if (comb && j < K) {
-      cinv[j] = inv[(tid >> 4) * K + j];
-      cw[j] = topk_w[(tid >> 4) * K + j];
+      cinv[j] = inv[a0 + (tid >> 4) * K + j];
+      cw[j] = topk_w[a0 + (tid >> 4) * K + j];
     }
   }
-  const int p = inv[m];
+  const int p = m < nt * K ? inv[a0 + m] : -1;
   if (p >= 0) {
-    const int e = topk_idx[m];
+    const int e = topk_idx[a0 + m];
     const int cl = (KC * 2 * half) >> 2, ch = (KC * 2 * (half + 1)) >> 2;  // chains 2h and 2h+1
     const size_t cell = (size_t)(I >> 4) * 256;
     const int8_t* bp = w2 + ((size_t)e * (D >> 4) + dt) * cell + lane * 16;
@@ -1027,16 +1034,16 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int D, int 
 #pragma unroll
       for (int c = 0; c < KCMAX; ++c) {
         if (cl + c >= c0 && cl + c < c1) {
-          uint4 a0 = uint4{0, 0, 0, 0}, a1 = uint4{0, 0, 0, 0};
+          uint4 a0v = uint4{0, 0, 0, 0}, a1v = uint4{0, 0, 0, 0};
           if (row0) {
             const uint4* ap = reinterpret_cast<const uint4*>(hr + (cl + c) * 64 + koff);
-            a0 = ap[0];
-            a1 = ap[1];
+            a0v = ap[0];
+            a1v = ap[1];
           }
           bf16x8 b0, b1;
           dequant16(q[c], sc, b0, b1);
-          acc[rr] = mfma16(as_bf16x8(a0), b0, acc[rr]);
-          acc[rr] = mfma16(as_bf16x8(a1), b1, acc[rr]);
+          acc[rr] = mfma16(as_bf16x8(a0v), b0, acc[rr]);
+          acc[rr] = mfma16(as_bf16x8(a1v), b1, acc[rr]);
         }
       }
     }
@@ -1063,7 +1070,7 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int D, int 
         acc = __builtin_fmaf(cw[j], y, acc);
       }
     }
-    const int64_t o = (int64_t)t * D + dt * 16 + col;
+    const int64_t o = (int64_t)(t0 + t) * D + dt * 16 + col;
     if (res) acc = bf16_bits_to_f32(res[o]) + round_bf16(acc);
     out[o] = f32_to_bf16_bits(acc);
   }
@@ -1249,10 +1256,11 @@ hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_
 }
 
 // the weights of a wave's chunks (half the reduction) stay in registers: at
-// most 12 chunks of 64
+// most 12 chunks of 64; a block holds the 8 / K tokens of up to 8 assignments
 bool down_combine_fits(const kmoe_desc& d) {
   const int64_t M = d.tokens * d.top_k, KC = d.intermediate / 64;
-  return M >= 1 && M <= kDownCombineMaxRows && KC <= 24 && M * d.intermediate * 2 <= 65536;
+  return d.top_k >= 1 && d.top_k <= kDownCombineMaxRows && M <= kDownCombineMaxAssignments && KC <= 24 &&
+         (int64_t)kDownCombineMaxRows * d.intermediate * 2 <= 65536;
 }
 
 hipError_t launch_down_combine(const kmoe_desc& d, const void* h_sorted, const int32_t* topk_idx, const int32_t* inv,
@@ -1260,19 +1268,20 @@ hipError_t launch_down_combine(const kmoe_desc& d, const void* h_sorted, const i
                                const void* res) {
   const int T = (int)d.tokens, K = (int)d.top_k, D = (int)d.hidden, I = (int)d.intermediate;
   if (!down_combine_fits(d)) return hipErrorInvalidValue;
-  const dim3 grid(D / 16), block(128 * T * K);
-  const size_t lds = (size_t)T * K * I * 2;
+  const int TPB = std::min(T, kDownCombineMaxRows / K);
+  const dim3 grid(D / 16, (T + TPB - 1) / TPB), block(128 * TPB * K);
+  const size_t lds = (size_t)TPB * K * I * 2;
   const uint16_t* hb = reinterpret_cast<const uint16_t*>(h_sorted);
   const int8_t* w2 = reinterpret_cast<const int8_t*>(p.w2);
   const float* s2 = reinterpret_cast<const float*>(p.s2);
   uint16_t* ob = reinterpret_cast<uint16_t*>(out);
   const uint16_t* rb = reinterpret_cast<const uint16_t*>(res);
   if (I / 64 <= 12)
-    hipLaunchKernelGGL((k_down_combine<6>), grid, block, lds, st, T, K, D, I, hb, topk_idx, inv, topk_w, w2, s2, ob,
-                       rb);
+    hipLaunchKernelGGL((k_down_combine<6>), grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w, w2, s2,
+                       ob, rb);
   else
-    hipLaunchKernelGGL((k_down_combine<12>), grid, block, lds, st, T, K, D, I, hb, topk_idx, inv, topk_w, w2, s2, ob,
-                       rb);
+    hipLaunchKernelGGL((k_down_combine<12>), grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w, w2, s2,
+                       ob, rb);
   return hipGetLastError();
 }
 

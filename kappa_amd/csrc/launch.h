@@ -57,9 +57,10 @@ hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, 
 // out = round(sum_j w * y_sorted[inv]) [+ residual res, rounded again], res may be NULL
 hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
                           hipStream_t st, const void* res = nullptr);
-// Packed decode with T * K <= 8 (down_combine_fits): the down projection and
-// the combine (with residual res, may be NULL) in one kernel; out is
-// bit-identical to the packed decode down kernel followed by launch_combine.
+// Packed decode with T * K <= 32 and K <= 8 (down_combine_fits): the down
+// projection and the combine (with residual res, may be NULL) in one kernel;
+// out is bit-identical to the packed decode down kernel followed by
+// launch_combine.
 bool down_combine_fits(const kmoe_desc& d);
 hipError_t launch_down_combine(const kmoe_desc& d, const void* h_sorted, const int32_t* topk_idx, const int32_t* inv,
                                const float* topk_w, const kmoe_packed_experts& p, void* out, hipStream_t st,

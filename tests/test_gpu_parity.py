@@ -272,7 +272,7 @@ def test_whole_block_matches_staged_path(dev, l30, T):
 @pytest.mark.parametrize("T,K", [(1, 8), (2, 4), (2, 8), (3, 8), (8, 8)])
 def test_whole_block_with_drops_matches_staged_path(dev, l30, T, K):
     """Capacity 1 under a skewed router drops assignments whenever two tokens
-    pick one expert; at T * K <= 8 the whole-block call runs the down
+    pick one expert; at T * K <= 32 the whole-block call runs the down
     projection and the combine as one kernel, which must skip the dropped rows
     exactly as the staged combine does and give the staged output bit for
     bit."""
@@ -295,12 +295,12 @@ def test_whole_block_with_drops_matches_staged_path(dev, l30, T, K):
     assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
 
 
-@pytest.mark.parametrize("T,K", [(1, 1), (1, 8), (3, 2), (4, 2), (8, 1), (2, 3)])
+@pytest.mark.parametrize("T,K", [(1, 1), (1, 8), (3, 2), (4, 2), (8, 1), (2, 3), (2, 8), (3, 8), (4, 8), (13, 2), (5, 6)])
 def test_fused_down_combine_shapes(dev, l30, T, K):
-    """The whole-block call at T * K <= 8 (down projection and combine in one
-    kernel, two waves per assignment, T * 16 combine threads) against the
-    staged calls, bit for bit, over the token/top-k splits of eight
-    assignments and fewer."""
+    """The whole-block call at T * K <= 32 (down projection and combine in one
+    kernel; blocks of 8 / K tokens, two waves per assignment, 16 combine
+    threads per token; a last block with fewer tokens) against the staged
+    calls, bit for bit."""
     from kappa_amd.qwen3 import moe_stages
     from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _moe_forward
 
@@ -321,7 +321,7 @@ def test_decode_batch_invariance(dev, l30, T):
     """A token's output does not depend on the other tokens of the call: the
     first T rows of a (T + 1)-token call equal the T-token call bit for bit.
     The pairs cross the kernel-shape switches of the decode path that keep the
-    summation order (fused down + combine up to T * K = 8, the dense token
+    summation order (fused down + combine up to T * K = 32, the dense token
     tile of the gate/up kernel up to T = 4, the one-block finish + dispatch up
     to T = 4 and T = 16). Between T = 16 and 17 the
     gate/up reduction goes from eight wave chains to four, a different
