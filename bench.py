@@ -303,11 +303,13 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # the first ~100 steps after the weight build run ~6% slower (clocks and
+    # caches settling); 200 untimed steps cost ~25 ms
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--prefill-tokens", type=int, default=4096)
-    ap.add_argument("--sweep", action="store_true", help="also time decode T in {1, 8, 32}")
+    ap.add_argument("--sweep", action="store_true", help="also time decode T in {1, 8, 32} and prefill T in {512, 2048}")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument(
@@ -458,7 +460,7 @@ def main():
         xp = [torch.randn(Tp, D, generator=gp, device=dev).to(torch.bfloat16) for _ in range(2)]
         op = [torch.empty(Tp, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
         psteps = max(10, args.steps // 5)
-        s = time_forward(bp, xp, op, psteps, 3)
+        s = time_forward(bp, xp, op, psteps, 10)
         gms, Up = time_gate_up(bp, xp, psteps, decode=False)
         Mp = Tp * K
         flops_gu = 2.0 * Mp * D * 2 * I
@@ -483,6 +485,23 @@ def main():
             },
         }
         result["prefill"]["library_reference"] = library_reference(Tp, D, I, E, K)
+        if args.sweep:
+            # the other prefill chunk sizes: whole-layer tokens/s and MFMA fraction
+            psweep = {}
+            for Tq in (512, 2048):
+                bq = [Bound(b.layer, Tq) for b in bounds[:2]]
+                xq = [x_[:Tq].contiguous() for x_ in xp]
+                oq = [o_[:Tq] for o_ in op]
+                sq = time_forward(bq, xq, oq, psteps, 10)
+                fq = 2.0 * Tq * K * 3 * D * I + 2.0 * Tq * D * E
+                psweep[str(Tq)] = {
+                    "tokens_per_s": Tq * psteps / sq,
+                    "us_per_step": sq * 1e6 / psteps,
+                    "layer_tflops": fq / (sq / psteps) / 1e12,
+                    "layer_mfma_frac": fq / (sq / psteps) / 1e12 / BF16_PEAK_TFLOPS,
+                }
+                log(f"bench: prefill T={Tq}: {psweep[str(Tq)]}")
+            result["prefill"]["sweep"] = psweep
         log(f"bench: prefill {result['prefill']}")
 
     if not args.no_cpu_baseline:
