@@ -20,6 +20,7 @@ constexpr int kMaxTopK = 64;
 constexpr int kMaxRouterSlices = 64;  // D <= 4096
 // Decode kernels keep up to this many 16-row blocks of one expert in registers.
 constexpr int kDecodeMaxRowBlocks = 4;  // T <= 64 tokens
+constexpr int kRowsPathMaxTokens = 128;  // above the decode sizes, the row-group kernels up to this T
 constexpr int kDownCombineMaxRows = 8;          // assignments per block of the fused decode down + combine
 constexpr int kDownCombineMaxAssignments = 32;  // T * K it takes
 

@@ -130,7 +130,7 @@ __device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
 // the expert are stored. The activation loads then depend on nothing and are
 // issued first, ahead of the expert lookup.
 // ---------------------------------------------------------------------------
-template <int WPB, int NB, bool GUARD, int MRB, bool DENSE>
+template <int WPB, int NB, bool GUARD, int MRB, bool DENSE, bool ALLROWS>
 __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int E, const uint16_t* __restrict__ x,
                                                         const int32_t* __restrict__ offsets,
                                                         const int32_t* __restrict__ active,
@@ -138,6 +138,7 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
                                                         const int8_t* __restrict__ w13, const float* __restrict__ s13,
                                                         uint16_t* __restrict__ h_sorted, int cap) {
   static_assert(!DENSE || (MRB == 1 && !GUARD), "dense tiles: one row block, one batch per wave");
+  static_assert(!ALLROWS || (!DENSE && !GUARD), "row groups: gathered rows, one batch per wave");
   __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][MRB][2][64];
   __shared__ int srt[16];  // DENSE: the tokens of the expert's rows
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -181,106 +182,116 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
   const float su = s13[(((size_t)e * IG + ig) * 2 + 1) * 16 + (lane & 15)];
   const int r0 = offsets[e];
   const int nrows = min(offsets[e + 1] - r0, cap);
-  const int nrb = DENSE ? 1 : min((nrows + 15) >> 4, MRB);
   if (DENSE && wv == 0 && lane < nrows) srt[lane] = sorted_token[r0 + lane];
-  const uint16_t* xr[MRB];
-  if (!DENSE) {
+  // ALLROWS: the expert's rows in groups of MRB 16-row blocks, the weights of
+  // the wave's single load batch kept in registers across the groups
+  const int ngroups = ALLROWS ? (nrows + 16 * MRB - 1) / (16 * MRB) : 1;
+  for (int grp = 0; grp < ngroups; ++grp) {
+    const int rbase = grp * 16 * MRB;
+    const int nrb = DENSE ? 1 : min((nrows - rbase + 15) >> 4, MRB);
+    const uint16_t* xr[MRB];
+    if (!DENSE) {
 #pragma unroll
-    for (int rb = 0; rb < MRB; ++rb) {
-      const int row = rb * 16 + (lane & 15);
-      const int tok = sorted_token[r0 + min(row, nrows - 1)];
-      xr[rb] = row < nrows ? x + (size_t)tok * D + koff : nullptr;
+      for (int rb = 0; rb < MRB; ++rb) {
+        const int row = rbase + rb * 16 + (lane & 15);
+        const int tok = sorted_token[r0 + min(row, nrows - 1)];
+        xr[rb] = row < nrows ? x + (size_t)tok * D + koff : nullptr;
+      }
     }
-  }
-  floatx4 ag[MRB], au[MRB];
-#pragma unroll
-  for (int rb = 0; rb < MRB; ++rb) {
-    ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
-    au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
-  }
-  for (int cb = c0; cb < c1; cb += NB) {
-    if (cb != c0) load_w(cb);
+    floatx4 ag[MRB], au[MRB];
 #pragma unroll
     for (int rb = 0; rb < MRB; ++rb) {
-      if (rb < nrb) {
-        uint4 a0[NB], a1[NB];
+      ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int cb = c0; cb < c1; cb += NB) {
+      if (cb != c0) load_w(cb);
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
+      for (int rb = 0; rb < MRB; ++rb) {
+        if (rb < nrb) {
+          uint4 a0[NB], a1[NB];
+#pragma unroll
+          for (int i = 0; i < NB; ++i) {
+            if (DENSE) {
+              a0[i] = da0[i];
+              a1[i] = da1[i];
+              continue;
+            }
+            a0[i] = uint4{0, 0, 0, 0};
+            a1[i] = uint4{0, 0, 0, 0};
+            if (xr[rb] && (!GUARD || cb + i < c1)) {
+              const uint4* ap = reinterpret_cast<const uint4*>(xr[rb] + (cb + i) * 64);
+              a0[i] = ap[0];
+              a1[i] = ap[1];
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < NB; ++i) {
+            if (!GUARD || cb + i < c1) {
+              bf16x8 bg0, bg1, bu0, bu1;
+              dequant16(qg[i], sg, bg0, bg1);
+              dequant16(qu[i], su, bu0, bu1);
+              ag[rb] = mfma16(as_bf16x8(a0[i]), bg0, ag[rb]);
+              ag[rb] = mfma16(as_bf16x8(a1[i]), bg1, ag[rb]);
+              au[rb] = mfma16(as_bf16x8(a0[i]), bu0, au[rb]);
+              au[rb] = mfma16(as_bf16x8(a1[i]), bu1, au[rb]);
+            }
+          }
+        }
+      }
+    }
+    if (wv > 0) {
+#pragma unroll
+      for (int rb = 0; rb < MRB; ++rb) {
+        if (rb < nrb) {
+          red[wv - 1][rb][0][lane] = ag[rb];
+          red[wv - 1][rb][1][lane] = au[rb];
+        }
+      }
+    }
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+      for (int rb = 0; rb < MRB; ++rb) {
+        if (rb >= nrb) break;
+        floatx4 g = ag[rb], u = au[rb];
+#pragma unroll
+        for (int w = 0; w < WPB - 1; ++w) {
+          g += red[w][rb][0][lane];
+          u += red[w][rb][1][lane];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = rbase + rb * 16 + 4 * (lane >> 4) + j;
+          // DENSE: tile row = token; find its position among the expert's rows
+          int pos = row < nrows ? r0 + row : -1;
           if (DENSE) {
-            a0[i] = da0[i];
-            a1[i] = da1[i];
-            continue;
+            pos = -1;
+            for (int r = 0; r < nrows; ++r)
+              if (srt[r] == row) pos = r0 + r;
           }
-          a0[i] = uint4{0, 0, 0, 0};
-          a1[i] = uint4{0, 0, 0, 0};
-          if (xr[rb] && (!GUARD || cb + i < c1)) {
-            const uint4* ap = reinterpret_cast<const uint4*>(xr[rb] + (cb + i) * 64);
-            a0[i] = ap[0];
-            a1[i] = ap[1];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-          if (!GUARD || cb + i < c1) {
-            bf16x8 bg0, bg1, bu0, bu1;
-            dequant16(qg[i], sg, bg0, bg1);
-            dequant16(qu[i], su, bu0, bu1);
-            ag[rb] = mfma16(as_bf16x8(a0[i]), bg0, ag[rb]);
-            ag[rb] = mfma16(as_bf16x8(a1[i]), bg1, ag[rb]);
-            au[rb] = mfma16(as_bf16x8(a0[i]), bu0, au[rb]);
-            au[rb] = mfma16(as_bf16x8(a1[i]), bu1, au[rb]);
+          if (pos >= 0) {
+            const float gv = round_bf16(g[j]), uv = round_bf16(u[j]);
+            h_sorted[(size_t)pos * I + ig * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(gv) * uv);
           }
         }
       }
     }
-  }
-  if (wv > 0) {
-#pragma unroll
-    for (int rb = 0; rb < MRB; ++rb) {
-      if (rb < nrb) {
-        red[wv - 1][rb][0][lane] = ag[rb];
-        red[wv - 1][rb][1][lane] = au[rb];
-      }
-    }
-  }
-  __syncthreads();
-  if (wv != 0) return;
-#pragma unroll
-  for (int rb = 0; rb < MRB; ++rb) {
-    if (rb >= nrb) break;
-    floatx4 g = ag[rb], u = au[rb];
-#pragma unroll
-    for (int w = 0; w < WPB - 1; ++w) {
-      g += red[w][rb][0][lane];
-      u += red[w][rb][1][lane];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = rb * 16 + 4 * (lane >> 4) + j;
-      // DENSE: tile row = token; find its position among the expert's rows
-      int pos = row < nrows ? r0 + row : -1;
-      if (DENSE) {
-        pos = -1;
-        for (int r = 0; r < nrows; ++r)
-          if (srt[r] == row) pos = r0 + r;
-      }
-      if (pos >= 0) {
-        const float gv = round_bf16(g[j]), uv = round_bf16(u[j]);
-        h_sorted[(size_t)pos * I + ig * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(gv) * uv);
-      }
-    }
+    // the reduction stage is reused by the next group
+    if (ALLROWS) __syncthreads();
   }
 }
 
 // Down projection for decode: one block per (active expert, NCG*16 output
 // columns), the reduction axis (I) split over the four waves; same load order
 // as the gate/up kernel.
-template <int WPB, int NCG, int NB, bool GUARD>
+template <int WPB, int NCG, int NB, bool GUARD, bool ALLROWS>
 __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const uint16_t* __restrict__ h_sorted,
                                                       const int32_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ active,
                                                       const int8_t* __restrict__ w2, const float* __restrict__ s2,
                                                       uint16_t* __restrict__ y_sorted, int cap) {
+  static_assert(!ALLROWS || !GUARD, "row groups: one batch per wave");
   __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][kDecodeMaxRowBlocks][NCG][64];
   const int dt = blockIdx.x;  // NCG*16 output columns
   const int slot = blockIdx.y;
@@ -306,74 +317,83 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
   for (int cg = 0; cg < NCG; ++cg) sc[cg] = s2[(size_t)e * D + (dt * NCG + cg) * 16 + (lane & 15)];
   const int r0 = offsets[e];
   const int nrows = min(offsets[e + 1] - r0, cap);
-  const int nrb = min((nrows + 15) >> 4, kDecodeMaxRowBlocks);
   const int koff = 16 * (lane >> 4);
-  const uint16_t* hr[kDecodeMaxRowBlocks];
-#pragma unroll
-  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
-    const int row = rb * 16 + (lane & 15);
-    hr[rb] = row < nrows ? h_sorted + (size_t)(r0 + row) * I + koff : nullptr;
-  }
-  floatx4 acc[kDecodeMaxRowBlocks][NCG];
-#pragma unroll
-  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb)
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) acc[rb][cg] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int cb = c0; cb < c1; cb += NB) {
-    if (cb != c0) load_w(cb);
+  // ALLROWS: the expert's rows in groups of kDecodeMaxRowBlocks 16-row blocks,
+  // the weights of the wave's single load batch kept in registers
+  const int ngroups = ALLROWS ? (nrows + 16 * kDecodeMaxRowBlocks - 1) / (16 * kDecodeMaxRowBlocks) : 1;
+  for (int grp = 0; grp < ngroups; ++grp) {
+    const int rbase = grp * 16 * kDecodeMaxRowBlocks;
+    const int nrb = min((nrows - rbase + 15) >> 4, kDecodeMaxRowBlocks);
+    const uint16_t* hr[kDecodeMaxRowBlocks];
 #pragma unroll
     for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
-      if (rb < nrb) {
-        uint4 a0[NB], a1[NB];
+      const int row = rbase + rb * 16 + (lane & 15);
+      hr[rb] = row < nrows ? h_sorted + (size_t)(r0 + row) * I + koff : nullptr;
+    }
+    floatx4 acc[kDecodeMaxRowBlocks][NCG];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-          a0[i] = uint4{0, 0, 0, 0};
-          a1[i] = uint4{0, 0, 0, 0};
-          if (hr[rb] && (!GUARD || cb + i < c1)) {
-            const uint4* ap = reinterpret_cast<const uint4*>(hr[rb] + (cb + i) * 64);
-            a0[i] = ap[0];
-            a1[i] = ap[1];
+    for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb)
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) acc[rb][cg] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int cb = c0; cb < c1; cb += NB) {
+      if (cb != c0) load_w(cb);
+#pragma unroll
+      for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+        if (rb < nrb) {
+          uint4 a0[NB], a1[NB];
+#pragma unroll
+          for (int i = 0; i < NB; ++i) {
+            a0[i] = uint4{0, 0, 0, 0};
+            a1[i] = uint4{0, 0, 0, 0};
+            if (hr[rb] && (!GUARD || cb + i < c1)) {
+              const uint4* ap = reinterpret_cast<const uint4*>(hr[rb] + (cb + i) * 64);
+              a0[i] = ap[0];
+              a1[i] = ap[1];
+            }
           }
-        }
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-          if (!GUARD || cb + i < c1) {
+          for (int i = 0; i < NB; ++i) {
+            if (!GUARD || cb + i < c1) {
 #pragma unroll
-            for (int cg = 0; cg < NCG; ++cg) {
-              bf16x8 b0, b1;
-              dequant16(q[i][cg], sc[cg], b0, b1);
-              acc[rb][cg] = mfma16(as_bf16x8(a0[i]), b0, acc[rb][cg]);
-              acc[rb][cg] = mfma16(as_bf16x8(a1[i]), b1, acc[rb][cg]);
+              for (int cg = 0; cg < NCG; ++cg) {
+                bf16x8 b0, b1;
+                dequant16(q[i][cg], sc[cg], b0, b1);
+                acc[rb][cg] = mfma16(as_bf16x8(a0[i]), b0, acc[rb][cg]);
+                acc[rb][cg] = mfma16(as_bf16x8(a1[i]), b1, acc[rb][cg]);
+              }
             }
           }
         }
       }
     }
-  }
-  if (wv > 0) {
+    if (wv > 0) {
 #pragma unroll
-    for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb)
-      if (rb < nrb)
+      for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb)
+        if (rb < nrb)
 #pragma unroll
-        for (int cg = 0; cg < NCG; ++cg) red[wv - 1][rb][cg][lane] = acc[rb][cg];
-  }
-  __syncthreads();
-  if (wv != 0) return;
+          for (int cg = 0; cg < NCG; ++cg) red[wv - 1][rb][cg][lane] = acc[rb][cg];
+    }
+    __syncthreads();
+    if (wv == 0) {
 #pragma unroll
-  for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
-    if (rb >= nrb) break;
+      for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
+        if (rb >= nrb) break;
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      floatx4 v = acc[rb][cg];
+        for (int cg = 0; cg < NCG; ++cg) {
+          floatx4 v = acc[rb][cg];
 #pragma unroll
-      for (int w = 0; w < WPB - 1; ++w) v += red[w][rb][cg][lane];
+          for (int w = 0; w < WPB - 1; ++w) v += red[w][rb][cg][lane];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = rb * 16 + 4 * (lane >> 4) + j;
-        if (row < nrows)
-          y_sorted[(size_t)(r0 + row) * D + (dt * NCG + cg) * 16 + (lane & 15)] = f32_to_bf16_bits(v[j]);
+          for (int j = 0; j < 4; ++j) {
+            const int row = rbase + rb * 16 + 4 * (lane >> 4) + j;
+            if (row < nrows)
+              y_sorted[(size_t)(r0 + row) * D + (dt * NCG + cg) * 16 + (lane & 15)] = f32_to_bf16_bits(v[j]);
+          }
+        }
       }
     }
+    // the reduction stage is reused by the next group
+    if (ALLROWS) __syncthreads();
   }
 }
 
@@ -1115,22 +1135,22 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
         // (DENSE); beyond, gathering only the expert's rows reads less.
         const bool dense = T <= 4;
         if (D / 64 == 32 && dense)
-          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, true>), grid, dim3(512), 0, st, T, D, I, E, xb, offsets,
+          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, true, false>), grid, dim3(512), 0, st, T, D, I, E, xb, offsets,
                              active, sorted_token, w13, s13, hb, cap);
         else if (D / 64 == 32)
-          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, false>), grid, dim3(512), 0, st, T, D, I, E, xb,
+          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, false, false>), grid, dim3(512), 0, st, T, D, I, E, xb,
                              offsets, active, sorted_token, w13, s13, hb, cap);
         else if (dense)
-          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, true>), grid, dim3(512), 0, st, T, D, I, E, xb, offsets,
+          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, true, false>), grid, dim3(512), 0, st, T, D, I, E, xb, offsets,
                              active, sorted_token, w13, s13, hb, cap);
         else
-          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, false>), grid, dim3(512), 0, st, T, D, I, E, xb,
+          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, false, false>), grid, dim3(512), 0, st, T, D, I, E, xb,
                              offsets, active, sorted_token, w13, s13, hb, cap);
       } else if ((D / 64) % 16 == 0) {
-        hipLaunchKernelGGL((k_gateup_decode<4, 4, false, kDecodeMaxRowBlocks, false>), grid, dim3(256), 0, st, T, D,
+        hipLaunchKernelGGL((k_gateup_decode<4, 4, false, kDecodeMaxRowBlocks, false, false>), grid, dim3(256), 0, st, T, D,
                            I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
       } else {
-        hipLaunchKernelGGL((k_gateup_decode<4, 4, true, kDecodeMaxRowBlocks, false>), grid, dim3(256), 0, st, T, D, I,
+        hipLaunchKernelGGL((k_gateup_decode<4, 4, true, kDecodeMaxRowBlocks, false, false>), grid, dim3(256), 0, st, T, D, I,
                            E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
       }
       hipError_t err = hipGetLastError();
@@ -1140,11 +1160,39 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
       const int cpw = (I / 64) / 4;
       const dim3 grid(D / 32, slots);
       if ((I / 64) % 4 == 0 && cpw % 3 == 0)
-        hipLaunchKernelGGL((k_down_decode<4, 2, 3, false>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
+        hipLaunchKernelGGL((k_down_decode<4, 2, 3, false, false>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
                            s2, yb, cap);
       else
-        hipLaunchKernelGGL((k_down_decode<4, 2, 4, true>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
+        hipLaunchKernelGGL((k_down_decode<4, 2, 4, true, false>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
                            s2, yb, cap);
+      return hipGetLastError();
+    }
+    return hipSuccess;
+  }
+  if (T <= kRowsPathMaxTokens && (D / 64 == 32 || D / 64 == 64) && (I / 64 == 12 || I / 64 == 24)) {
+    // just above the decode sizes: the decode kernels over all of an expert's
+    // rows in groups of 64, each wave's weights loaded once and kept in
+    // registers (65 and 128 tokens: 158 -> 143 and 161 -> 155 us per layer
+    // against the grouped GEMMs; from 256 tokens on the GEMMs are faster)
+    if (stages & kStageGateUp) {
+      const dim3 grid(I / 16, slots);
+      if (D / 64 == 32)
+        hipLaunchKernelGGL((k_gateup_decode<4, 8, false, kDecodeMaxRowBlocks, false, true>), grid, dim3(256), 0, st, T,
+                           D, I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
+      else
+        hipLaunchKernelGGL((k_gateup_decode<8, 8, false, kDecodeMaxRowBlocks, false, true>), grid, dim3(512), 0, st, T,
+                           D, I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
+      hipError_t err = hipGetLastError();
+      if (err != hipSuccess) return err;
+    }
+    if (stages & kStageDown) {
+      const dim3 grid(D / 32, slots);
+      if (I / 64 == 12)
+        hipLaunchKernelGGL((k_down_decode<4, 2, 3, false, true>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active,
+                           w2, s2, yb, cap);
+      else
+        hipLaunchKernelGGL((k_down_decode<4, 2, 6, false, true>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active,
+                           w2, s2, yb, cap);
       return hipGetLastError();
     }
     return hipSuccess;

@@ -195,6 +195,20 @@ def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48):
     return od
 
 
+@pytest.mark.parametrize("T", [65, 100, 128])
+def test_30b_rows_path(dev, l30, T):
+    """65..128 tokens run the decode kernels over all of an expert's rows in
+    groups of 64 (the skewed router puts more than 64 rows on its hot experts,
+    so those take several groups): routing bit-exact, sampled rows and h/y
+    against the oracle."""
+    _prefill_sampled(l30, T, seed=500 + T, n_tok=24)
+    x = make_x(T, l30.D, seed=600 + T)
+    x[:, 0] = 1.0
+    router = skew_router(l30.router, lam=1.5)
+    od = _prefill_sampled(l30, T, seed=600 + T, router=router, x=x, n_tok=24)
+    assert int(np.max(od["group_sizes"])) > 64 or T < 100
+
+
 def test_30b_skewed_routing(dev, l30):
     for T, seed in ((4096, 7), (64, 8)):
         x = make_x(T, l30.D, seed=seed)
@@ -210,6 +224,7 @@ def test_235b_layer(dev):
 
     layer = make_layer("235b", seed=1)
     _prefill_sampled(layer, 16, seed=16, n_tok=16)
+    _prefill_sampled(layer, 100, seed=100, n_tok=16)  # the row-group kernels
     _prefill_sampled(layer, 2048, seed=2048, n_tok=24)
     # T = 1 and 2: the whole layer (fused down + combine at T = 1, each wave
     # holding 12 of the 24 chunks of the reduction) against the staged calls
