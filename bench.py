@@ -17,6 +17,8 @@ Prints ONE JSON line on stdout (logs go to stderr):
   prefill      the 4096-token prefill chunk: tokens/s and the MFMA roofline
                of its dominant kernel (the gate/up grouped GEMM), next to
                hipBLASLt bf16 GEMMs of the same shapes (library_reference)
+  --sweep      also decode T in {1, 8, 32}, prefill T in {512, 2048}, and the
+               235B-A22B-shaped layer (decode T=16, prefill T=2048)
   cpu_baseline the oracle (the C restatement of the reference algorithm),
                OpenMP on this host's cores, on a bounded sample
 """
@@ -219,6 +221,61 @@ def measured_traffic(kernel: str, workload: str):
     except OSError:
         pass
     return None
+
+
+def bench_235b(bounds, xs, outs, args, dev):
+    """The 235B-A22B-shaped W8 layer (D 4096, E 128, K 8, I 1536, ~2.4 GB of
+    int8 experts): decode T=16 (HBM fraction) and prefill T=2048 (MFMA
+    fraction), two weight copies in rotation. Frees the 30B copies first."""
+    import torch
+
+    from kappa_amd.qwen3 import moe_stages
+    from moe_cases import make_layer
+
+    bounds.clear()
+    xs.clear()
+    outs.clear()
+    torch.cuda.empty_cache()
+    log("bench: building 2 weight copies of the 235B-A22B W8 layer")
+    big = [make_layer("235b", seed=40 + i) for i in range(2)]
+    D, E, K, I = big[0].D, big[0].E, big[0].K, big[0].I
+    res = {}
+    for T, kind in ((16, "decode"), (2048, "prefill")):
+        bb = [Bound(layer, T) for layer in big]
+        g = torch.Generator(device=dev)
+        g.manual_seed(13)
+        xb = [torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(2)]
+        ob = [torch.empty(T, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+        steps = args.steps if kind == "decode" else max(10, args.steps // 5)
+        secs = time_forward(bb, xb, ob, steps, args.warmup if kind == "decode" else 10)
+        step_s = secs / steps
+        if kind == "decode":
+            us_ = [
+                int(torch.unique(moe_stages.route(x, b.layer.router, num_experts=E, k=K)["idx"]).numel())
+                for b, x in zip(bb, xb)
+            ]
+            U = sum(us_) / len(us_)
+            lb = U * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 4 * T * D
+            res["decode_T16"] = {
+                "us_per_step": step_s * 1e6,
+                "tokens_per_s": T / step_s,
+                "layer_hbm_gbs": lb / step_s / 1e9,
+                "layer_hbm_frac": lb / step_s / 1e9 / HBM_PEAK_GBS,
+                "active_experts": U,
+            }
+        else:
+            fl = 2.0 * T * K * 3 * D * I + 2.0 * T * D * E
+            res["prefill_T2048"] = {
+                "us_per_step": step_s * 1e6,
+                "tokens_per_s": T / step_s,
+                "layer_tflops": fl / step_s / 1e12,
+                "layer_mfma_frac": fl / step_s / 1e12 / BF16_PEAK_TFLOPS,
+            }
+        log(f"bench: 235B {kind} T={T}: {step_s * 1e6:.1f} us/step")
+        del bb, xb, ob
+    del big
+    torch.cuda.empty_cache()
+    return res
 
 
 def library_reference(T, D, I, E, K, reps=20):
@@ -510,6 +567,9 @@ def main():
         log(f"bench: cpu {result['cpu_baseline']}")
     else:
         result["cpu_baseline"] = None
+
+    if args.sweep:
+        result["layer_235b"] = bench_235b(bounds, xs, outs, args, dev)
     print(json.dumps(result), flush=True)
 
 
