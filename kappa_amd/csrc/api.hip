@@ -121,7 +121,7 @@ Workspace layout(const kmoe_desc& d) {
   w.inv = take(4 * M);
   w.h_sorted = take(act * M * I);
   w.y_sorted = take(act * M * D);
-  w.route_part = take(T <= (size_t)kmoe::kDispatchBlock ? 4 * kmoe_host::route_split_part_floats(d) : 0);
+  w.route_part = take(T <= (size_t)kmoe_host::kSplitRouterMaxTokens ? 4 * kmoe_host::route_split_part_floats(d) : 0);
   w.normed = take(act * T * D);  // rms_norm(h) for kmoe_forward_block
   w.total = o;
   return w;
@@ -328,7 +328,7 @@ kmoe_status check_forward_args(const kmoe_desc* desc, const kmoe_weight* router,
 
 // The stage sequence of moe_swiglu_ffn on x. With a norm, x is the residual
 // stream h: the block runs on h2 = rms_norm(h) (norm->h2, computed by the
-// split router at T <= 64, else by the norm kernel) and the combine adds the
+// split router at T <= 128, else by the norm kernel) and the combine adds the
 // block's rounded output to h.
 kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host::SliceNorm* norm,
                            const kmoe_weight* router, const kmoe_weight* gate, const kmoe_weight* up,
@@ -347,17 +347,21 @@ kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host
   int32_t* inv = reinterpret_cast<int32_t*>(base + w.inv);
   void* hs = base + w.h_sorted;
   void* ys = base + w.y_sorted;
-  if (desc->tokens <= kmoe::kDispatchBlock) {
-    // one 64-token chunk: the split router (normalising its input rows when
-    // there is a norm, and running the dispatch sort itself at T <= 4); the
-    // dispatch counts the chunk itself
+  if (desc->tokens <= kmoe_host::kSplitRouterMaxTokens) {
+    // the split router (normalising its input rows when there is a norm, and
+    // running the dispatch sort itself at T <= 16); one 64-token chunk counts
+    // itself in the dispatch, two need the chunk histograms first
     float* part = reinterpret_cast<float*>(base + w.route_part);
     const kmoe_host::DispatchOut dout{gs, off, act, stok, sexp, inv};
     KMOE_HIP(kmoe_host::launch_route_split(*desc, x, *router, part, nullptr, tidx, tw, st, norm, &dout),
              "route kernels");
-    if (!kmoe_host::split_router_dispatches(*desc))
+    if (desc->tokens > kmoe::kDispatchBlock) {
+      KMOE_HIP(kmoe_host::launch_dispatch_count(*desc, tidx, hist, st), "dispatch count kernel");
+      KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, hist, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
+    } else if (!kmoe_host::split_router_dispatches(*desc)) {
       KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, nullptr, gs, off, act, stok, sexp, inv, st),
                "dispatch kernel");
+    }
   } else {
     if (norm)
       KMOE_HIP(kmoe_host::launch_rms_norm(*desc, x, norm->scale, norm->scale_bf16 ? KMOE_DTYPE_BF16 : KMOE_DTYPE_F32,

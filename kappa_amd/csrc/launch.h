@@ -10,6 +10,10 @@ namespace kmoe_host {
 // route.hip
 hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* logits, int32_t* topk_idx,
                         float* topk_w, int32_t* hist, hipStream_t st);
+// per-64-token-chunk expert histograms of the selections (for launch_dispatch)
+hipError_t launch_dispatch_count(const kmoe_desc& d, const int32_t* topk_idx, int32_t* hist, hipStream_t st);
+// The whole-block call routes up to this many tokens with the split router.
+constexpr int kSplitRouterMaxTokens = 128;
 // Split router (many blocks per token; same logits and selections as
 // launch_route): part holds route_split_part_floats(d) floats of workspace.
 // With a SliceNorm, x is the residual stream h: the router reduces and

@@ -873,6 +873,10 @@ hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& r,
     route_rt<float>(d, rs, x, r, logits, topk_idx, topk_w, st);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !hist) return err;
+  return launch_dispatch_count(d, topk_idx, hist, st);
+}
+
+hipError_t launch_dispatch_count(const kmoe_desc& d, const int32_t* topk_idx, int32_t* hist, hipStream_t st) {
   const int T = (int)d.tokens, E = (int)d.num_experts, K = (int)d.top_k;
   const int nblk = (T + kDispatchBlock - 1) / kDispatchBlock;
   hipLaunchKernelGGL(k_dispatch_count, dim3(nblk), dim3(256), 0, st, T, E, K, topk_idx, hist);

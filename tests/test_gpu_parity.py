@@ -258,12 +258,14 @@ def test_decode_and_prefill_kernels_agree_at_threshold(dev, l30):
         check_out(outs[0], outs[1], True, f"T={T}")
 
 
-@pytest.mark.parametrize("T", [1, 2, 8, 16, 17, 40, 64])
+@pytest.mark.parametrize("T", [1, 2, 8, 16, 17, 40, 64, 65, 100, 128])
 def test_whole_block_matches_staged_path(dev, l30, T):
-    """At T <= 64 the whole-block call routes with the split router (many blocks
-    per token); the staged calls use the one-block-per-token router. Both follow
-    the canonical summation order, so selections, weights and outputs are
-    bit-identical. The skewed router puts up to 64 rows on an expert."""
+    """At T <= 128 the whole-block call routes with the split router (many
+    blocks per token); the staged calls use the one-block-per-token router.
+    Both follow the canonical summation order, so selections, weights and
+    outputs are bit-identical. The skewed router puts up to T rows on an
+    expert (above 64 tokens: two dispatch chunks, and row groups in the
+    expert kernels)."""
     from kappa_amd.qwen3 import moe_stages
     from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _moe_forward
 
