@@ -265,11 +265,13 @@ def bench_235b(bounds, xs, outs, args, dev):
             }
         else:
             fl = 2.0 * T * K * 3 * D * I + 2.0 * T * D * E
+            lb = E * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 4 * T * D
             res["prefill_T2048"] = {
                 "us_per_step": step_s * 1e6,
                 "tokens_per_s": T / step_s,
                 "layer_tflops": fl / step_s / 1e12,
                 "layer_mfma_frac": fl / step_s / 1e12 / BF16_PEAK_TFLOPS,
+                "layer_hbm_frac": lb / step_s / 1e9 / HBM_PEAK_GBS,
             }
         log(f"bench: 235B {kind} T={T}: {step_s * 1e6:.1f} us/step")
         del bb, xb, ob
@@ -551,11 +553,14 @@ def main():
                 oq = [o_[:Tq] for o_ in op]
                 sq = time_forward(bq, xq, oq, psteps, 10)
                 fq = 2.0 * Tq * K * 3 * D * I + 2.0 * Tq * D * E
+                # every expert is active at these sizes: the weight stream bounds T=512
+                bq_ = E * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 4 * Tq * D
                 psweep[str(Tq)] = {
                     "tokens_per_s": Tq * psteps / sq,
                     "us_per_step": sq * 1e6 / psteps,
                     "layer_tflops": fq / (sq / psteps) / 1e12,
                     "layer_mfma_frac": fq / (sq / psteps) / 1e12 / BF16_PEAK_TFLOPS,
+                    "layer_hbm_frac": bq_ / (sq / psteps) / 1e9 / HBM_PEAK_GBS,
                 }
                 log(f"bench: prefill T={Tq}: {psweep[str(Tq)]}")
             result["prefill"]["sweep"] = psweep
