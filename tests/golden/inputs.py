@@ -135,7 +135,7 @@ def digest(inputs: dict) -> str:
     return h.hexdigest()
 
 
-# Golden cases. Shapes follow the reference's own checks and the BASELINE configs:
+# Golden cases. Shapes follow the reference's own checks and the benchmark workloads:
 #   verify_f32:  scripts/verify_qwen3_moe_impls.py:23 (b=2,t=3,d=16,e=8,k=2,i=32, fp32)
 #   toy_f32:     the CPU-runnable toy block (T=64, D=256, E=8, K=2, I=128, fp32, N(0,0.02))
 #   w8c_*:       small W8 per-channel bf16 blocks (the 30B layer's numerics at toy size)
