@@ -98,7 +98,7 @@ def _norm_scale(D, seed, dev):
     return torch.from_numpy((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)).to(dev).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("T", [1, 8, 64, 65, 4096])
+@pytest.mark.parametrize("T", [1, 2, 8, 17, 64, 65, 128, 129, 4096])
 def test_30b_fused_block_equals_separate_calls(dev, l30, T):
     """moe_block_ffn == h + moe_swiglu_ffn(rms_norm(h)), bit for bit; the norm is
     checked against the oracle on every row, the MoE half against the oracle
@@ -125,7 +125,7 @@ def test_30b_fused_block_fixed_capacity(dev, l30):
         hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_impl="fixed_capacity",
         moe_capacity_factor=0.5,
     )  # fmt: skip
-    for T in (64, 1024):
+    for T in (3, 64, 100, 1024):
         h = make_x(T, l30.D, seed=950 + T).reshape(1, T, l30.D)
         sc = _norm_scale(l30.D, 7 + T, dev)
         composed = h + moe_swiglu_ffn(rms_norm(h, sc), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
