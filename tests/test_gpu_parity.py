@@ -229,6 +229,14 @@ def test_235b_layer(dev):
     # T = 1 and 2: the whole layer (fused down + combine at T = 1, each wave
     # holding 12 of the 24 chunks of the reduction) against the staged calls
     cfg = moe_layer_config(hidden=layer.D, experts=layer.E, top_k=layer.K, intermediate=layer.I)
+    # the block call at T = 100: the split router normalising 4096-wide rows
+    # (four tokens per block)
+    from kappa_amd.qwen3 import moe_block_ffn, rms_norm
+
+    h = make_x(100, layer.D, seed=101).reshape(1, 100, layer.D)
+    sc = (1.0 + 0.1 * torch.randn(layer.D, device=dev)).to(torch.bfloat16)
+    composed = h + moe_swiglu_ffn(rms_norm(h, sc), layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
+    assert torch.equal(moe_block_ffn(h, sc, layer.router, layer.gate, layer.up, layer.down, cfg=cfg), composed)
     for T in (1, 2):
         _prefill_sampled(layer, T, seed=T, n_tok=T)
         x = make_x(T, layer.D, seed=T)
