@@ -49,7 +49,7 @@ def log(*a):
 class Bound:
     """One layer copy with every C struct prebuilt, so a step is one ctypes call."""
 
-    def __init__(self, layer, T, threshold=64):
+    def __init__(self, layer, T, impl="ragged_jax", threshold=0):
         import torch
 
         from kappa_amd import _lib
@@ -59,7 +59,8 @@ class Bound:
         self.layer = layer
         dev = layer.router.device
         self.T = T
-        self.desc = _desc(T, layer.D, layer.E, layer.K, layer.I, torch.bfloat16, threshold)
+        # per-channel W8: the ragged program at every token count (ragged_jax, threshold 0)
+        self.desc = _desc(T, layer.D, layer.E, layer.K, layer.I, torch.bfloat16, impl=impl, threshold=threshold)
         self.r, self._kr = weight_struct(layer.router, dev, n_out=layer.E, n_groups=None, name="router")
         self.g, self._kg = weight_struct(layer.gate, dev, n_out=layer.I, n_groups=layer.E, name="gate")
         self.u, self._ku = weight_struct(layer.up, dev, n_out=layer.I, n_groups=layer.E, name="up")
@@ -175,7 +176,7 @@ def time_gate_up(bounds, xs, steps, decode: bool):
         x = xs[i % len(xs)]
         r = moe_stages.route(x, lay.router, num_experts=lay.E, k=lay.K)
         dsp = moe_stages.dispatch(r["idx"], r["hist"], num_experts=lay.E)
-        h = torch.empty((x.shape[0] * lay.K, lay.I), dtype=torch.bfloat16, device=x.device)
+        h = torch.empty((x.shape[0] * lay.K, 2 * lay.I), dtype=torch.bfloat16, device=x.device)  # hi, lo planes
         items.append((b, x, dsp, h))
         actives.append(dsp["active"][lay.E : lay.E + 1])
     for it in items:
@@ -197,9 +198,12 @@ def _gate_up_only(b, x, dsp, h, decode):
 
     from kappa_amd import _lib
 
+    from kappa_amd.qwen3.ffn_moe import _desc
+
     lay = b.layer
     T = x.shape[0]
-    desc = type(b.desc)(T, lay.D, lay.E, lay.K, lay.I, 1, 64 if decode else 0, 0)
+    desc = _desc(T, lay.D, lay.E, lay.K, lay.I, torch.bfloat16, impl="ragged_jax", threshold=0,
+                 kernels=_lib.KERNELS_AUTO if decode else _lib.KERNELS_GROUPED)  # fmt: skip
     _lib.check(
         _lib.lib().kmoe_expert_gate_up(
             desc, x.data_ptr(), dsp["offsets"].data_ptr(), dsp["active"].data_ptr(), dsp["sorted_token"].data_ptr(),
@@ -324,12 +328,14 @@ def cpu_baseline(layer, T, budget_s=12.0, max_reps=20):
     x = layer_x_host(T, layer.D)
     threads = len(os.sched_getaffinity(0))
     oracle.set_threads(threads)
-    oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True)  # warm
+    oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True,
+                   impl="ragged")  # warm  # fmt: skip
     times = []
     t_start = time.perf_counter()
     while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
         t0 = time.perf_counter()
-        oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True)
+        oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True,
+                       impl="ragged")  # fmt: skip
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     cpu = ""

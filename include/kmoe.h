@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define KMOE_ABI_VERSION 2
+#define KMOE_ABI_VERSION 3
 
 typedef enum kmoe_status {
   KMOE_OK = 0,
@@ -59,6 +59,35 @@ typedef enum kmoe_scale_kind {
   KMOE_SCALE_CHANNEL = 2   /* one scale per (expert, output channel): [E, 1, N] */
 } kmoe_scale_kind;
 
+/* The array program of the layer, cfg.moe_impl (MoEImpl, kappa/qwen3/architecture.py:14).
+ * Each has its own rounding points, which the kernels follow:
+ *   GATHER_EINSUM   _moe_gather_einsum (kappa/qwen3/ffn_moe.py:74-104): weights
+ *                   bf16(q * bf16(s)); g, u, every step of silu(g) * u and y in x.dtype;
+ *                   out = round(sum_k f32(round(y_k * w_k))). Takes plain weights or one
+ *                   scale per tensor (moe_take_dequant, kappa/qwen3/quant.py:71-74, does not
+ *                   broadcast [E, 1, N] scales against the gathered [T, K, D, I] values).
+ *   RAGGED          _moe_ragged (:174-216; ragged_jax and ragged_tokamax): weights
+ *                   q * s and g, u, h, y in f32; y rounded to x.dtype; the products
+ *                   round(y * w) added into a zero buffer of x.dtype in j order, each add
+ *                   rounded. With T <= decode_token_threshold the layer runs
+ *                   GATHER_EINSUM instead (_effective_moe_impl, :219-223).
+ *   FIXED_CAPACITY  _moe_fixed_capacity (:107-158): the GATHER_EINSUM expert chain on
+ *                   each expert's first expert_capacity assignments, the RAGGED combine. */
+typedef enum kmoe_impl {
+  KMOE_IMPL_GATHER_EINSUM = 0,
+  KMOE_IMPL_RAGGED = 1,
+  KMOE_IMPL_FIXED_CAPACITY = 2
+} kmoe_impl;
+
+/* Kernel family of the expert products. Every family follows the impl's rounding
+ * points; they add the same products in different f32 orders, so results agree to
+ * rounding but are not bit-identical across families. */
+typedef enum kmoe_kernels {
+  KMOE_KERNELS_AUTO = 0,     /* by token count: GEMV-style up to 64 tokens, row groups up to 128, grouped GEMMs above */
+  KMOE_KERNELS_DECODE = 1,   /* the GEMV-style kernels (at most 128 tokens)           */
+  KMOE_KERNELS_GROUPED = 2   /* the grouped GEMMs at any token count                  */
+} kmoe_kernels;
+
 /* A weight operand: `Weight = Array | Q8Weight(values, scale)`
  * (kappa/qwen3/quant.py:15-22). For int8 values the dequantised weight is
  * values * scale with the scale first cast to the compute dtype
@@ -80,14 +109,15 @@ typedef struct kmoe_desc {
   int64_t top_k;                  /* K = num_experts_per_tok                   */
   int64_t intermediate;           /* I = moe intermediate size                 */
   kmoe_dtype act_dtype;           /* F32 or BF16 (x.dtype)                     */
-  int64_t decode_token_threshold; /* T <= this uses the decode kernels
-                                     (moe_ragged_decode_token_threshold, :49) */
-  int64_t expert_capacity;        /* 0: dropless (gather_einsum / ragged paths).
-                                     > 0: fixed_capacity token dropping: an assignment
+  kmoe_impl impl;                 /* cfg.moe_impl                              */
+  int64_t decode_token_threshold; /* moe_ragged_decode_token_threshold (:49):
+                                     impl RAGGED with T <= this runs GATHER_EINSUM */
+  int64_t expert_capacity;        /* impl FIXED_CAPACITY: the slot limit
+                                     min(c_dyn, c_buf) >= 1 (:136-141); an assignment
                                      whose slot within its expert's stable order is
                                      >= this is dropped and adds nothing to its
-                                     token's output (kappa/qwen3/ffn_moe.py:107-158;
-                                     the caller passes min(c_dyn, c_buf), :136-141) */
+                                     token's output. 0 for the other impls. */
+  kmoe_kernels kernels;           /* kernel family (AUTO: by token count)      */
 } kmoe_desc;
 
 /* W8 expert weights relaid out once, at load time, for the gfx950 kernels
@@ -95,14 +125,20 @@ typedef struct kmoe_desc {
  * kappa/qwen3/weights.py:143-188). All four buffers are caller-owned device
  * memory of the sizes kmoe_prepack_bytes() reports:
  *   w13 [E][I/16][2][D/16][16][16] int8  gate (0) and up (1), 16 columns x 16 k per cell
- *   s13 [E][I/16][2][16]           f32   their scales, already rounded to bf16
+ *   s13 [E][I/16][2][16]           f32   their scales as given (a scalar is repeated)
  *   w2  [E][D/16][I/16][16][16]    int8  down
- *   s2  [E][D]                     f32   its scales, already rounded to bf16 */
+ *   s2  [E][D]                     f32   its scales
+ * The caller also records the shapes the buffers hold and the kind of the source
+ * scales; a forward call checks them against its desc and impl. */
 typedef struct kmoe_packed_experts {
   void* w13;
   void* s13;
   void* w2;
   void* s2;
+  int64_t num_experts;              /* E */
+  int64_t hidden;                   /* D */
+  int64_t intermediate;             /* I */
+  kmoe_scale_kind source_scale_kind; /* TENSOR if all three source scales were scalars, else CHANNEL */
 } kmoe_packed_experts;
 
 typedef struct kmoe_packed_sizes {
@@ -126,9 +162,12 @@ kmoe_status kmoe_prepack_bytes(const kmoe_desc* desc, kmoe_packed_sizes* sizes);
 
 /* --- whole block ---------------------------------------------------------- */
 /* moe_swiglu_ffn (kappa/qwen3/ffn_moe.py:226-299): router, top-k with
- * renormalisation, dispatch, SwiGLU experts and the weighted combine.
+ * renormalisation, dispatch, SwiGLU experts and the weighted combine, with the
+ * rounding points of desc->impl (after the decode switch, :219-223).
  * `packed` may be NULL: int8 experts then run on the layout-native kernels.
- * topk_idx_out [T,K] int32 and topk_w_out [T,K] (x dtype) are optional. */
+ * topk_idx_out [T,K] int32 and topk_w_out [T,K] (x dtype) are optional.
+ * GATHER_EINSUM with per-channel scales and more than one expert is
+ * KMOE_ERR_INVALID_ARG: the reference's gather program cannot apply them. */
 kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight* router, const kmoe_weight* gate,
                          const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed, void* out,
                          int32_t* topk_idx_out, void* topk_w_out, void* workspace, size_t workspace_bytes,
@@ -174,7 +213,9 @@ kmoe_status kmoe_dispatch(const kmoe_desc* desc, const int32_t* topk_idx, const 
                           int32_t* sorted_expert, int32_t* inv, void* stream);
 
 /* SwiGLU experts over the sorted rows (kappa/qwen3/ffn_moe.py:99-102,
- * 207-210): h_sorted [T*K, I] and y_sorted [T*K, D] in x.dtype. */
+ * 149-152, 207-210): y_sorted [T*K, D] in x.dtype; h_sorted [T*K, I] in x.dtype,
+ * except for the RAGGED chain with bf16 activations, whose f32 h is stored as
+ * [T*K, 2I] bf16: per row hi = bf16(h) in [0, I) and lo = bf16(h - hi) in [I, 2I). */
 kmoe_status kmoe_expert_ffn(const kmoe_desc* desc, const void* x, const int32_t* offsets, const int32_t* active,
                             const int32_t* sorted_token, const int32_t* sorted_expert, const kmoe_weight* gate,
                             const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed,
@@ -192,8 +233,10 @@ kmoe_status kmoe_expert_down(const kmoe_desc* desc, const void* h_sorted, const 
                              const int32_t* active, const int32_t* sorted_expert, const kmoe_weight* down,
                              const kmoe_packed_experts* packed, void* y_sorted, void* stream);
 
-/* Weighted combine (kappa/qwen3/ffn_moe.py:103, 213-215), atomic-free:
- * out[t] = round(sum_{j<K} topk_w[t,j] * y_sorted[inv[t*K+j]]). */
+/* Weighted combine (kappa/qwen3/ffn_moe.py:103, 155-157, 213-215), atomic-free,
+ * with the terms p_j = round(topk_w[t,j] * y_sorted[inv[t*K+j]]) in j order:
+ * GATHER_EINSUM out[t] = round(sum_j p_j) (f32 sum); RAGGED and FIXED_CAPACITY
+ * out[t] = round(...round(round(p_0) + p_1)... + p_{K-1}). inv < 0 skips a term. */
 kmoe_status kmoe_combine(const kmoe_desc* desc, const void* y_sorted, const int32_t* inv, const float* topk_w,
                          void* out, void* stream);
 

@@ -31,6 +31,18 @@ SCALE_NONE = 0
 SCALE_TENSOR = 1
 SCALE_CHANNEL = 2
 
+# kmoe_impl
+IMPL_GATHER_EINSUM = 0
+IMPL_RAGGED = 1
+IMPL_FIXED_CAPACITY = 2
+
+# kmoe_kernels
+KERNELS_AUTO = 0
+KERNELS_DECODE = 1
+KERNELS_GROUPED = 2
+
+ABI_VERSION = 3
+
 # Every symbol include/kmoe.h declares.
 EXPORTS = (
     "kmoe_version",
@@ -73,13 +85,24 @@ class KmoeDesc(ctypes.Structure):
         ("top_k", ctypes.c_int64),
         ("intermediate", ctypes.c_int64),
         ("act_dtype", ctypes.c_int),
+        ("impl", ctypes.c_int),
         ("decode_token_threshold", ctypes.c_int64),
         ("expert_capacity", ctypes.c_int64),
+        ("kernels", ctypes.c_int),
     ]
 
 
 class KmoePacked(ctypes.Structure):
-    _fields_ = [("w13", ctypes.c_void_p), ("s13", ctypes.c_void_p), ("w2", ctypes.c_void_p), ("s2", ctypes.c_void_p)]
+    _fields_ = [
+        ("w13", ctypes.c_void_p),
+        ("s13", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("s2", ctypes.c_void_p),
+        ("num_experts", ctypes.c_int64),
+        ("hidden", ctypes.c_int64),
+        ("intermediate", ctypes.c_int64),
+        ("source_scale_kind", ctypes.c_int),
+    ]
 
 
 class KmoePackedSizes(ctypes.Structure):
@@ -166,6 +189,10 @@ def lib() -> ctypes.CDLL:
                     )
                 L = ctypes.CDLL(LIB_PATH)
                 _declare(L)
+                if L.kmoe_abi_version() != ABI_VERSION:
+                    raise ImportError(
+                        f"{LIB_PATH} has ABI {L.kmoe_abi_version()}, this binding expects {ABI_VERSION}: rebuild it"
+                    )
                 _lib = L
     return _lib
 

@@ -57,8 +57,42 @@ kmoe_status check_desc(const kmoe_desc* d) {
                 kmoe::kRouterSlice * kmoe::kMaxRouterSlices);
   if (d->tokens * d->top_k > (int64_t)0x7fffffff || d->tokens * d->hidden > ((int64_t)1 << 40))
     return fail(KMOE_ERR_UNSUPPORTED, "tokens %lld too large", (long long)d->tokens);
-  if (d->expert_capacity < 0)
-    return fail(KMOE_ERR_INVALID_ARG, "expert_capacity must be >= 0 (got %lld)", (long long)d->expert_capacity);
+  if (d->impl != KMOE_IMPL_GATHER_EINSUM && d->impl != KMOE_IMPL_RAGGED && d->impl != KMOE_IMPL_FIXED_CAPACITY)
+    return fail(KMOE_ERR_INVALID_ARG, "unknown impl %d", (int)d->impl);
+  if (d->impl == KMOE_IMPL_FIXED_CAPACITY && d->expert_capacity < 1)
+    return fail(KMOE_ERR_INVALID_ARG, "fixed_capacity needs expert_capacity >= 1 (got %lld)",
+                (long long)d->expert_capacity);
+  if (d->impl != KMOE_IMPL_FIXED_CAPACITY && d->expert_capacity != 0)
+    return fail(KMOE_ERR_INVALID_ARG, "expert_capacity must be 0 unless impl is fixed_capacity (got %lld)",
+                (long long)d->expert_capacity);
+  if (d->kernels != KMOE_KERNELS_AUTO && d->kernels != KMOE_KERNELS_DECODE && d->kernels != KMOE_KERNELS_GROUPED)
+    return fail(KMOE_ERR_INVALID_ARG, "unknown kernels %d", (int)d->kernels);
+  if (d->kernels == KMOE_KERNELS_DECODE && d->tokens > kmoe::kRowsPathMaxTokens)
+    return fail(KMOE_ERR_UNSUPPORTED, "the decode kernels take at most %d tokens (got %lld)", kmoe::kRowsPathMaxTokens,
+                (long long)d->tokens);
+  return KMOE_OK;
+}
+
+// _effective_moe_impl (kappa/qwen3/ffn_moe.py:219-223)
+kmoe_impl effective_impl(const kmoe_desc& d) {
+  if (d.impl == KMOE_IMPL_RAGGED && d.tokens <= d.decode_token_threshold) return KMOE_IMPL_GATHER_EINSUM;
+  return d.impl;
+}
+
+// the expert products' rounding chain and the combine of the program that runs
+int chain_of(const kmoe_desc& d) {
+  return effective_impl(d) == KMOE_IMPL_RAGGED ? kmoe::kChainF32 : kmoe::kChainAct;
+}
+bool scatter_of(const kmoe_desc& d) { return effective_impl(d) != KMOE_IMPL_GATHER_EINSUM; }
+
+// The gather program multiplies the gathered [T, K, D, I] values by the scale as
+// stored (kappa/qwen3/quant.py:71-74): a per-tensor scale, or [E, 1, N] with E = 1.
+kmoe_status check_gather_scales(const kmoe_desc& d, kmoe_scale_kind kind, const char* name) {
+  if (effective_impl(d) == KMOE_IMPL_GATHER_EINSUM && kind == KMOE_SCALE_CHANNEL && d.num_experts > 1)
+    return fail(KMOE_ERR_INVALID_ARG,
+                "%s: gather_einsum takes one scale per tensor; per-channel scales of %lld experts run with the "
+                "ragged or fixed_capacity impl",
+                name, (long long)d.num_experts);
   return KMOE_OK;
 }
 
@@ -119,7 +153,8 @@ Workspace layout(const kmoe_desc& d) {
   w.sorted_token = take(4 * M);
   w.sorted_expert = take(4 * M);
   w.inv = take(4 * M);
-  w.h_sorted = take(act * M * I);
+  // the f32 chain keeps h as two bf16 planes per row for bf16 activations
+  w.h_sorted = take((chain_of(d) == kmoe::kChainF32 && d.act_dtype == KMOE_DTYPE_BF16 ? 4 : act) * M * I);
   w.y_sorted = take(act * M * D);
   w.route_part = take(T <= (size_t)kmoe_host::kSplitRouterMaxTokens ? 4 * kmoe_host::route_split_part_floats(d) : 0);
   w.normed = take(act * T * D);  // rms_norm(h) for kmoe_forward_block
@@ -129,11 +164,17 @@ Workspace layout(const kmoe_desc& d) {
 
 bool packed_ok(const kmoe_desc& d, const kmoe_packed_experts* p) {
   return p && p->w13 && p->s13 && p->w2 && p->s2 && d.act_dtype == KMOE_DTYPE_BF16 && d.hidden % 64 == 0 &&
-         d.intermediate % 64 == 0;
+         d.intermediate % 64 == 0 && p->num_experts == d.num_experts && p->hidden == d.hidden &&
+         p->intermediate == d.intermediate;
 }
 
-bool decode_path(const kmoe_desc& d) {
-  return d.tokens <= d.decode_token_threshold && d.tokens <= 16 * kmoe::kDecodeMaxRowBlocks;
+// The GEMV-style kernels up to 64 tokens (the decode batches), their row-group
+// form up to 128 tokens, the grouped GEMMs above (or whenever asked for).
+int family_of(const kmoe_desc& d) {
+  if (d.kernels == KMOE_KERNELS_GROUPED) return kmoe_host::kFamilyGemm;
+  if (d.tokens <= 16 * kmoe::kDecodeMaxRowBlocks) return kmoe_host::kFamilyDecode;
+  if (d.tokens <= kmoe::kRowsPathMaxTokens) return kmoe_host::kFamilyRows;
+  return kmoe_host::kFamilyGemm;
 }
 
 kmoe_status expert_stage(const kmoe_desc& d, int stages, const void* x, const int32_t* offsets, const int32_t* active,
@@ -142,11 +183,11 @@ kmoe_status expert_stage(const kmoe_desc& d, int stages, const void* x, const in
                          void* h_sorted, void* y_sorted, hipStream_t st) {
   hipError_t e;
   if (packed_ok(d, packed)) {
-    e = kmoe_host::launch_expert_packed(d, decode_path(d), stages, x, offsets, active, sorted_token, *packed,
-                                        h_sorted, y_sorted, st);
+    e = kmoe_host::launch_expert_packed(d, chain_of(d), family_of(d), stages, x, offsets, active, sorted_token,
+                                        *packed, h_sorted, y_sorted, st);
   } else {
-    e = kmoe_host::launch_expert_generic(d, stages, x, sorted_token, sorted_expert, gate, up, down, h_sorted,
-                                         y_sorted, st);
+    e = kmoe_host::launch_expert_generic(d, chain_of(d), stages, x, sorted_token, sorted_expert, gate, up, down,
+                                         h_sorted, y_sorted, st);
   }
   if (e != hipSuccess) return hip_fail(e, "expert kernels");
   return KMOE_OK;
@@ -159,8 +200,13 @@ kmoe_status check_stage_weights(const kmoe_desc& d, const kmoe_packed_experts* p
   if (stages & kmoe_host::kStageGateUp) {
     KMOE_TRY(check_weight(gate, "gate"));
     KMOE_TRY(check_weight(up, "up"));
+    KMOE_TRY(check_gather_scales(d, gate->scale_kind, "gate"));
+    KMOE_TRY(check_gather_scales(d, up->scale_kind, "up"));
   }
-  if (stages & kmoe_host::kStageDown) KMOE_TRY(check_weight(down, "down"));
+  if (stages & kmoe_host::kStageDown) {
+    KMOE_TRY(check_weight(down, "down"));
+    KMOE_TRY(check_gather_scales(d, down->scale_kind, "down"));
+  }
   return KMOE_OK;
 }
 
@@ -172,6 +218,14 @@ kmoe_status check_packed_arg(const kmoe_desc& d, const kmoe_packed_experts* pack
     return fail(KMOE_ERR_UNSUPPORTED, "packed int8 experts run with bf16 activations only");
   if (d.hidden % 64 || d.intermediate % 64)
     return fail(KMOE_ERR_UNSUPPORTED, "packed experts need hidden and intermediate divisible by 64");
+  if (packed->num_experts != d.num_experts || packed->hidden != d.hidden || packed->intermediate != d.intermediate)
+    return fail(KMOE_ERR_INVALID_ARG,
+                "packed experts hold E=%lld, D=%lld, I=%lld; the call has E=%lld, D=%lld, I=%lld",
+                (long long)packed->num_experts, (long long)packed->hidden, (long long)packed->intermediate,
+                (long long)d.num_experts, (long long)d.hidden, (long long)d.intermediate);
+  if (packed->source_scale_kind != KMOE_SCALE_TENSOR && packed->source_scale_kind != KMOE_SCALE_CHANNEL)
+    return fail(KMOE_ERR_INVALID_ARG, "packed experts: source_scale_kind must be TENSOR or CHANNEL");
+  KMOE_TRY(check_gather_scales(d, packed->source_scale_kind, "packed experts"));
   return KMOE_OK;
 }
 
@@ -179,7 +233,7 @@ kmoe_status check_packed_arg(const kmoe_desc& d, const kmoe_packed_experts* pack
 
 extern "C" {
 
-const char* kmoe_version(void) { return "kmoe 0.1.0 (gfx950)"; }
+const char* kmoe_version(void) { return "kmoe 0.2.0 (gfx950)"; }
 
 int kmoe_abi_version(void) { return KMOE_ABI_VERSION; }
 
@@ -304,7 +358,7 @@ kmoe_status kmoe_combine(const kmoe_desc* desc, const void* y_sorted, const int3
   if (!y_sorted || !inv || !topk_w || !out) return fail(KMOE_ERR_INVALID_ARG, "kmoe_combine: NULL buffer");
   KMOE_TRY(device_status());
   if (desc->tokens == 0) return KMOE_OK;
-  hipError_t e = kmoe_host::launch_combine(*desc, y_sorted, inv, topk_w, out, (hipStream_t)stream);
+  hipError_t e = kmoe_host::launch_combine(*desc, scatter_of(*desc), y_sorted, inv, topk_w, out, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "combine kernel");
   return KMOE_OK;
 }
@@ -322,6 +376,9 @@ kmoe_status check_forward_args(const kmoe_desc* desc, const kmoe_weight* router,
     KMOE_TRY(check_weight(gate, "gate"));
     KMOE_TRY(check_weight(up, "up"));
     KMOE_TRY(check_weight(down, "down"));
+    KMOE_TRY(check_gather_scales(*desc, gate->scale_kind, "gate"));
+    KMOE_TRY(check_gather_scales(*desc, up->scale_kind, "up"));
+    KMOE_TRY(check_gather_scales(*desc, down->scale_kind, "down"));
   }
   return KMOE_OK;
 }
@@ -370,15 +427,19 @@ kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host
     KMOE_HIP(kmoe_host::launch_route(*desc, xin, *router, nullptr, tidx, tw, hist, st), "route kernels");
     KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, hist, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
   }
-  if (packed_ok(*desc, packed) && decode_path(*desc) && kmoe_host::down_combine_fits(*desc)) {
+  const int chain = chain_of(*desc);
+  const bool scatter = scatter_of(*desc);
+  if (packed_ok(*desc, packed) && family_of(*desc) == kmoe_host::kFamilyDecode &&
+      kmoe_host::down_combine_fits(*desc, chain)) {
     // at most 32 assignments: the down projection and the combine in one kernel
     KMOE_TRY(expert_stage(*desc, kmoe_host::kStageGateUp, xin, off, act, stok, sexp, gate, up, down, packed, hs, ys,
                           st));
-    KMOE_HIP(kmoe_host::launch_down_combine(*desc, hs, tidx, inv, tw, *packed, out, st, res), "down+combine kernel");
+    KMOE_HIP(kmoe_host::launch_down_combine(*desc, chain, scatter, hs, tidx, inv, tw, *packed, out, st, res),
+             "down+combine kernel");
   } else {
     KMOE_TRY(expert_stage(*desc, kmoe_host::kStageGateUp | kmoe_host::kStageDown, xin, off, act, stok, sexp, gate,
                           up, down, packed, hs, ys, st));
-    KMOE_HIP(kmoe_host::launch_combine(*desc, ys, inv, tw, out, st, res), "combine kernel");
+    KMOE_HIP(kmoe_host::launch_combine(*desc, scatter, ys, inv, tw, out, st, res), "combine kernel");
   }
   if (topk_idx_out)
     KMOE_HIP(hipMemcpyAsync(topk_idx_out, tidx, sizeof(int32_t) * desc->tokens * desc->top_k,
@@ -460,6 +521,9 @@ kmoe_status kmoe_prepack(const kmoe_desc* desc, const kmoe_weight* gate, const k
     return fail(KMOE_ERR_UNSUPPORTED, "kmoe_prepack packs int8 (Q8) experts only");
   if (!packed || !packed->w13 || !packed->s13 || !packed->w2 || !packed->s2)
     return fail(KMOE_ERR_INVALID_ARG, "kmoe_prepack: packed buffers must be non-NULL");
+  if (packed->num_experts != desc->num_experts || packed->hidden != desc->hidden ||
+      packed->intermediate != desc->intermediate)
+    return fail(KMOE_ERR_INVALID_ARG, "kmoe_prepack: the packed shapes must be the desc's E, D and I");
   if (desc->hidden % 64 || desc->intermediate % 64)
     return fail(KMOE_ERR_UNSUPPORTED, "packed experts need hidden and intermediate divisible by 64");
   KMOE_TRY(device_status());

@@ -56,8 +56,37 @@ struct Act<uint16_t> {
   __device__ __forceinline__ static void store(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16_bits(v); }
 };
 
-// silu(g) = g / (1 + exp(-g)) (jax.nn.silu, kappa/qwen3/ffn_moe.py:101)
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+// Rounding chain of the expert products (which array program runs):
+//   kChainAct: _moe_gather_einsum / _moe_fixed_capacity (kappa/qwen3/ffn_moe.py:99-102,
+//     146-152): weights bf16(q * bf16(s)), g, u, every step of silu(g) * u and y
+//     rounded to the activation dtype;
+//   kChainF32: _moe_ragged (:202-213): weights q * s in f32 (the scale applied to the
+//     f32 sum, a per-output-channel factor), g, u, h and the down sum in f32, only y
+//     rounded. With bf16 activations h is stored as two bf16 planes per row, hi =
+//     bf16(h) and lo = bf16(h - hi) ([M][2I]), which the MFMA down products take as
+//     two operands (hi + lo carries h to ~2^-17 relative).
+constexpr int kChainAct = 0;
+constexpr int kChainF32 = 1;
+
+// sigmoid(g) = 1 / (1 + exp(-g)) in f32 (jax.nn.sigmoid)
+__device__ __forceinline__ float sigmoid_f32(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// jax.nn.silu(g) * u (kappa/qwen3/ffn_moe.py:101, 151, 209) with silu(g) = g * sigmoid(g):
+// each product rounded to the activation dtype when R rounds (bf16), else f32.
+template <bool BF16>
+__device__ __forceinline__ float swiglu(float g, float u) {
+  if (BF16) {
+    const float sg = round_bf16(__fmul_rn(g, round_bf16(sigmoid_f32(g))));
+    return round_bf16(__fmul_rn(sg, u));
+  }
+  return __fmul_rn(__fmul_rn(g, sigmoid_f32(g)), u);
+}
+
+// h = hi + lo with hi = bf16(h), lo = bf16(h - hi) (h - hi is exact in f32)
+__device__ __forceinline__ void split_bf16(float h, uint16_t& hi, uint16_t& lo) {
+  hi = f32_to_bf16_bits(h);
+  lo = f32_to_bf16_bits(__fsub_rn(h, bf16_bits_to_f32(hi)));
+}
 
 __device__ __forceinline__ int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

@@ -1,13 +1,17 @@
 // SwiGLU experts over the dispatch-sorted rows, and the weighted combine.
 //
-// Reference: _moe_gather_einsum (kappa/qwen3/ffn_moe.py:74-104) for the
-// rounding points, _moe_ragged (kappa/qwen3/ffn_moe.py:174-216) for the
-// grouped form: every expert's weights are read once per row tile instead of
-// once per assignment.
+// Reference: the rounding points of the array program that runs
+// (_moe_gather_einsum kappa/qwen3/ffn_moe.py:74-104 and _moe_fixed_capacity
+// :107-158 on the kChainAct chain, _moe_ragged :174-216 on the kChainF32
+// chain), in the grouped form of _moe_ragged: every expert's weights are read
+// once per row tile instead of once per assignment.
 //
 // Packed int8 experts (bf16 activations) run on bf16 MFMA
-// (v_mfma_f32_16x16x32_bf16); int8 is dequantised in registers to
-// bf16(q * bf16(scale)) right after a coalesced 16-byte load. The MFMA k order
+// (v_mfma_f32_16x16x32_bf16); int8 is converted in registers right after a
+// coalesced 16-byte load, to bf16(q * bf16(scale)) for kChainAct and to the
+// exact integers for kChainF32, whose f32 per-column scale multiplies the f32
+// sum in the epilogue (q * s summed over k equals s * sum(q) up to f32
+// rounding, since the scale is constant along the reduction). The MFMA k order
 // inside a 64-wide chunk is permuted: lane l supplies k = 16*(l/16) + 8*s + 0..7
 // in sub-step s, for both operands, which matches the packed layout
 // [.., k/16, col, 16 k] where each lane's 16 bytes are one column's 16 k.
@@ -42,6 +46,38 @@ __device__ __forceinline__ void dequant16(const uint4 q, const float s, bf16x8& 
   }
   lo = __builtin_bit_cast(bf16x8, uint4{o[0], o[1], o[2], o[3]});
   hi = __builtin_bit_cast(bf16x8, uint4{o[4], o[5], o[6], o[7]});
+}
+
+// 16 int8 -> the same 16 integers in bf16 (exact: |q| <= 128 needs 8 bits), for the
+// f32 chain, which applies its f32 scale to the sum
+__device__ __forceinline__ void cvt16(const uint4 q, bf16x8& lo, bf16x8& hi) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t v = w[j >> 1];
+    const int sh = 16 * (j & 1);
+    o[j] = pack_bf16x2((float)(int8_t)((v >> sh) & 0xffu), (float)(int8_t)((v >> (sh + 8)) & 0xffu));
+  }
+  lo = __builtin_bit_cast(bf16x8, uint4{o[0], o[1], o[2], o[3]});
+  hi = __builtin_bit_cast(bf16x8, uint4{o[4], o[5], o[6], o[7]});
+}
+
+// The B operand of a 16-byte int8 load for chain CH: bf16(q * s) with s already
+// rounded to bf16 (kChainAct), or the exact integers (kChainF32).
+template <int CH>
+__device__ __forceinline__ void weights16(const uint4 q, const float s, bf16x8& lo, bf16x8& hi) {
+  if (CH == kChainAct)
+    dequant16(q, s, lo, hi);
+  else
+    cvt16(q, lo, hi);
+}
+
+// The packed scales are stored as given (f32); kChainAct casts them to bf16
+// first (kappa/qwen3/quant.py:37, 74).
+template <int CH>
+__device__ __forceinline__ float chain_scale(float s) {
+  return CH == kChainAct ? round_bf16(s) : s;
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -130,7 +166,7 @@ __device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
 // the expert are stored. The activation loads then depend on nothing and are
 // issued first, ahead of the expert lookup.
 // ---------------------------------------------------------------------------
-template <int WPB, int NB, bool GUARD, int MRB, bool DENSE, bool ALLROWS>
+template <int WPB, int NB, bool GUARD, int MRB, bool DENSE, bool ALLROWS, int CH>
 __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int E, const uint16_t* __restrict__ x,
                                                         const int32_t* __restrict__ offsets,
                                                         const int32_t* __restrict__ active,
@@ -178,8 +214,8 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
     }
   };
   load_w(c0);
-  const float sg = s13[(((size_t)e * IG + ig) * 2 + 0) * 16 + (lane & 15)];
-  const float su = s13[(((size_t)e * IG + ig) * 2 + 1) * 16 + (lane & 15)];
+  const float sg = chain_scale<CH>(s13[(((size_t)e * IG + ig) * 2 + 0) * 16 + (lane & 15)]);
+  const float su = chain_scale<CH>(s13[(((size_t)e * IG + ig) * 2 + 1) * 16 + (lane & 15)]);
   const int r0 = offsets[e];
   const int nrows = min(offsets[e + 1] - r0, cap);
   if (DENSE && wv == 0 && lane < nrows) srt[lane] = sorted_token[r0 + lane];
@@ -229,8 +265,8 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
           for (int i = 0; i < NB; ++i) {
             if (!GUARD || cb + i < c1) {
               bf16x8 bg0, bg1, bu0, bu1;
-              dequant16(qg[i], sg, bg0, bg1);
-              dequant16(qu[i], su, bu0, bu1);
+              weights16<CH>(qg[i], sg, bg0, bg1);
+              weights16<CH>(qu[i], su, bu0, bu1);
               ag[rb] = mfma16(as_bf16x8(a0[i]), bg0, ag[rb]);
               ag[rb] = mfma16(as_bf16x8(a1[i]), bg1, ag[rb]);
               au[rb] = mfma16(as_bf16x8(a0[i]), bu0, au[rb]);
@@ -271,8 +307,18 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
               if (srt[r] == row) pos = r0 + r;
           }
           if (pos >= 0) {
-            const float gv = round_bf16(g[j]), uv = round_bf16(u[j]);
-            h_sorted[(size_t)pos * I + ig * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(gv) * uv);
+            if (CH == kChainAct) {
+              const float gv = round_bf16(g[j]), uv = round_bf16(u[j]);
+              h_sorted[(size_t)pos * I + ig * 16 + (lane & 15)] = f32_to_bf16_bits(swiglu<true>(gv, uv));
+            } else {
+              // f32 g, u, h; h as its hi and lo planes (row stride 2I)
+              const float hv = swiglu<false>(__fmul_rn(g[j], sg), __fmul_rn(u[j], su));
+              uint16_t hi, lo;
+              split_bf16(hv, hi, lo);
+              uint16_t* hr = h_sorted + (size_t)pos * 2 * I + ig * 16 + (lane & 15);
+              hr[0] = hi;
+              hr[I] = lo;
+            }
           }
         }
       }
@@ -285,7 +331,7 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
 // Down projection for decode: one block per (active expert, NCG*16 output
 // columns), the reduction axis (I) split over the four waves; same load order
 // as the gate/up kernel.
-template <int WPB, int NCG, int NB, bool GUARD, bool ALLROWS>
+template <int WPB, int NCG, int NB, bool GUARD, bool ALLROWS, int CH>
 __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const uint16_t* __restrict__ h_sorted,
                                                       const int32_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ active,
@@ -314,7 +360,9 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
   load_w(c0);
   float sc[NCG];
 #pragma unroll
-  for (int cg = 0; cg < NCG; ++cg) sc[cg] = s2[(size_t)e * D + (dt * NCG + cg) * 16 + (lane & 15)];
+  for (int cg = 0; cg < NCG; ++cg) sc[cg] = chain_scale<CH>(s2[(size_t)e * D + (dt * NCG + cg) * 16 + (lane & 15)]);
+  // kChainF32: h rows hold the hi and lo planes (stride 2I)
+  const size_t hstride = CH == kChainF32 ? 2 * (size_t)I : (size_t)I;
   const int r0 = offsets[e];
   const int nrows = min(offsets[e + 1] - r0, cap);
   const int koff = 16 * (lane >> 4);
@@ -328,7 +376,7 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
 #pragma unroll
     for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
       const int row = rbase + rb * 16 + (lane & 15);
-      hr[rb] = row < nrows ? h_sorted + (size_t)(r0 + row) * I + koff : nullptr;
+      hr[rb] = row < nrows ? h_sorted + (size_t)(r0 + row) * hstride + koff : nullptr;
     }
     floatx4 acc[kDecodeMaxRowBlocks][NCG];
 #pragma unroll
@@ -340,26 +388,32 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
 #pragma unroll
       for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
         if (rb < nrb) {
-          uint4 a0[NB], a1[NB];
+          constexpr int NP = CH == kChainF32 ? 2 : 1;  // h planes
+          uint4 a0[NP][NB], a1[NP][NB];
 #pragma unroll
-          for (int i = 0; i < NB; ++i) {
-            a0[i] = uint4{0, 0, 0, 0};
-            a1[i] = uint4{0, 0, 0, 0};
-            if (hr[rb] && (!GUARD || cb + i < c1)) {
-              const uint4* ap = reinterpret_cast<const uint4*>(hr[rb] + (cb + i) * 64);
-              a0[i] = ap[0];
-              a1[i] = ap[1];
+          for (int pl = 0; pl < NP; ++pl)
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+              a0[pl][i] = uint4{0, 0, 0, 0};
+              a1[pl][i] = uint4{0, 0, 0, 0};
+              if (hr[rb] && (!GUARD || cb + i < c1)) {
+                const uint4* ap = reinterpret_cast<const uint4*>(hr[rb] + pl * I + (cb + i) * 64);
+                a0[pl][i] = ap[0];
+                a1[pl][i] = ap[1];
+              }
             }
-          }
 #pragma unroll
           for (int i = 0; i < NB; ++i) {
             if (!GUARD || cb + i < c1) {
 #pragma unroll
               for (int cg = 0; cg < NCG; ++cg) {
                 bf16x8 b0, b1;
-                dequant16(q[i][cg], sc[cg], b0, b1);
-                acc[rb][cg] = mfma16(as_bf16x8(a0[i]), b0, acc[rb][cg]);
-                acc[rb][cg] = mfma16(as_bf16x8(a1[i]), b1, acc[rb][cg]);
+                weights16<CH>(q[i][cg], sc[cg], b0, b1);
+#pragma unroll
+                for (int pl = 0; pl < NP; ++pl) {
+                  acc[rb][cg] = mfma16(as_bf16x8(a0[pl][i]), b0, acc[rb][cg]);
+                  acc[rb][cg] = mfma16(as_bf16x8(a1[pl][i]), b1, acc[rb][cg]);
+                }
               }
             }
           }
@@ -387,7 +441,8 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
           for (int j = 0; j < 4; ++j) {
             const int row = rbase + rb * 16 + 4 * (lane >> 4) + j;
             if (row < nrows)
-              y_sorted[(size_t)(r0 + row) * D + (dt * NCG + cg) * 16 + (lane & 15)] = f32_to_bf16_bits(v[j]);
+              y_sorted[(size_t)(r0 + row) * D + (dt * NCG + cg) * 16 + (lane & 15)] =
+                  f32_to_bf16_bits(CH == kChainF32 ? __fmul_rn(v[j], sc[cg]) : v[j]);
           }
         }
       }
@@ -436,7 +491,7 @@ __device__ __forceinline__ bool prefill_tile(const int32_t* __restrict__ offsets
 // GATEUP = true: A rows gathered from x by token, B = gate|up column groups,
 // epilogue SwiGLU -> h_sorted. GATEUP = false: A = h_sorted rows, B = down,
 // epilogue -> y_sorted.
-template <bool GATEUP>
+template <bool GATEUP, int CH>
 __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const uint16_t* __restrict__ src,
                                                      const int32_t* __restrict__ offsets,
                                                      const int32_t* __restrict__ sorted_token,
@@ -444,7 +499,10 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
                                                      uint16_t* __restrict__ dst, int cap) {
   __shared__ PrefillLds s;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int Kdim = GATEUP ? D : I;
+  // kChainF32 down: the A rows are h's hi and lo planes (2I wide), both against the
+  // same weight chunks
+  const int Kdim = GATEUP ? D : (CH == kChainF32 ? 2 * I : I);
+  const int KCW = (GATEUP ? D : I) >> 6;  // weight chunks along the reduction
   const int Ndim = GATEUP ? I : D;
   const int NT = GATEUP ? (I >> 6) : (D >> 7);
   int e, row0, rows, nt;
@@ -465,30 +523,31 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
     const int igl = nt * 4 + (cg & 3);
     const size_t cid = ((size_t)e * (I >> 4) + igl) * 2 + which;
     bp = wp + cid * (size_t)(D >> 4) * 256;
-    sc0 = sp[cid * 16 + (l0 & 15)];
-    sc1 = sp[cid * 16 + ((l0 + 1) & 15)];
+    sc0 = chain_scale<CH>(sp[cid * 16 + (l0 & 15)]);
+    sc1 = chain_scale<CH>(sp[cid * 16 + ((l0 + 1) & 15)]);
   } else {
     const int dg = nt * 8 + cg;
     bp = wp + ((size_t)e * (D >> 4) + dg) * (size_t)(I >> 4) * 256;
-    sc0 = sp[(size_t)e * D + dg * 16 + (l0 & 15)];
-    sc1 = sp[(size_t)e * D + dg * 16 + ((l0 + 1) & 15)];
+    sc0 = chain_scale<CH>(sp[(size_t)e * D + dg * 16 + (l0 & 15)]);
+    sc1 = chain_scale<CH>(sp[(size_t)e * D + dg * 16 + ((l0 + 1) & 15)]);
   }
 
   uint4 ra[4], rq[2];
   auto gload = [&](int c) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) ra[j] = ap ? reinterpret_cast<const uint4*>(ap + c * 64)[j] : uint4{0, 0, 0, 0};
-    rq[0] = *reinterpret_cast<const uint4*>(bp + (size_t)c * 1024 + l0 * 16);
-    rq[1] = *reinterpret_cast<const uint4*>(bp + (size_t)c * 1024 + (l0 + 1) * 16);
+    const int cw = c % KCW;
+    rq[0] = *reinterpret_cast<const uint4*>(bp + (size_t)cw * 1024 + l0 * 16);
+    rq[1] = *reinterpret_cast<const uint4*>(bp + (size_t)cw * 1024 + (l0 + 1) * 16);
   };
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(&s.a[buf][ar][ah * 32 + 8 * j]) = ra[j];
     bf16x8 lo, hi;
-    dequant16(rq[0], sc0, lo, hi);
+    weights16<CH>(rq[0], sc0, lo, hi);
     *reinterpret_cast<bf16x8*>(&s.b[buf][0][cg][l0][0]) = lo;
     *reinterpret_cast<bf16x8*>(&s.b[buf][1][cg][l0][0]) = hi;
-    dequant16(rq[1], sc1, lo, hi);
+    weights16<CH>(rq[1], sc1, lo, hi);
     *reinterpret_cast<bf16x8*>(&s.b[buf][0][cg][l0 + 1][0]) = lo;
     *reinterpret_cast<bf16x8*>(&s.b[buf][1][cg][l0 + 1][0]) = hi;
   };
@@ -543,17 +602,28 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
     for (int j = 0; j < 4; ++j) {
       const int row = wm * 64 + mi * 16 + 4 * (lane >> 4) + j;
       if (row >= rows) continue;
-      uint16_t* drow = dst + (size_t)(row0 + row) * Ndim;
+      uint16_t* drow = dst + (size_t)(row0 + row) * (GATEUP && CH == kChainF32 ? 2 * Ndim : Ndim);
       if (GATEUP) {
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) {
-          const float g = round_bf16(acc[mi][2 * ni][j]);
-          const float u = round_bf16(acc[mi][2 * ni + 1][j]);
-          drow[nt * 64 + wn * 32 + ni * 16 + (lane & 15)] = f32_to_bf16_bits(silu_f32(g) * u);
+          const int col = nt * 64 + wn * 32 + ni * 16 + (lane & 15);
+          if (CH == kChainAct) {
+            const float g = round_bf16(acc[mi][2 * ni][j]);
+            const float u = round_bf16(acc[mi][2 * ni + 1][j]);
+            drow[col] = f32_to_bf16_bits(swiglu<true>(g, u));
+          } else {
+            const size_t cid = ((size_t)e * (I >> 4) + (col >> 4)) * 2;
+            const float g = __fmul_rn(acc[mi][2 * ni][j], sp[cid * 16 + (lane & 15)]);
+            const float u = __fmul_rn(acc[mi][2 * ni + 1][j], sp[(cid + 1) * 16 + (lane & 15)]);
+            split_bf16(swiglu<false>(g, u), drow[col], drow[I + col]);
+          }
         }
       } else {
 #pragma unroll
-        for (int n = 0; n < 4; ++n) drow[nt * 128 + wn * 64 + n * 16 + (lane & 15)] = f32_to_bf16_bits(acc[mi][n][j]);
+        for (int n = 0; n < 4; ++n) {
+          const int col = nt * 128 + wn * 64 + n * 16 + (lane & 15);
+          drow[col] = f32_to_bf16_bits(CH == kChainF32 ? __fmul_rn(acc[mi][n][j], sp[(size_t)e * D + col]) : acc[mi][n][j]);
+        }
       }
     }
   }
@@ -611,31 +681,12 @@ __device__ __forceinline__ void vm_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// silu(g) * u for the MFMA epilogue: hardware exp2 and reciprocal (a few fp32
-// ulps from g / (1 + expf(-g)); the product is rounded to bf16 next).
-__device__ __forceinline__ float silu_mul_fast(float g, float u) {
-  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
-}
-
 // Element offset of 16-byte piece p of row r in an A stage: [row][8 x 16 B],
 // pieces XOR-swizzled by (r >> 1) & 7. A row is half the 256-byte bank width,
 // so this puts the 16 rows one fragment read touches on 16 distinct 16-byte
 // bank groups.
 __device__ __forceinline__ int a_piece(int r, int p) { return p ^ (r & 7); }
 __device__ __forceinline__ int a_swz(int r, int p) { return r * 64 + (a_piece(r, p) << 3); }
-
-// 8 int8 (two dwords) -> bf16(q * s), s already rounded to bf16
-__device__ __forceinline__ bf16x8 dequant8(const uint32_t w0, const uint32_t w1, const float s) {
-  const uint32_t w[2] = {w0, w1};
-  uint32_t o[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t v = w[j >> 1];
-    const int sh = 16 * (j & 1);
-    o[j] = pack_bf16x2((float)(int8_t)((v >> sh) & 0xffu) * s, (float)(int8_t)((v >> (sh + 8)) & 0xffu) * s);
-  }
-  return __builtin_bit_cast(bf16x8, uint4{o[0], o[1], o[2], o[3]});
-}
 
 constexpr int kGemmRows = 128;                // rows per tile
 constexpr int kGemmA = kGemmRows * 128;       // A stage: 128 rows x 64 bf16 (16 KB)
@@ -651,10 +702,12 @@ struct GemmLoads {
   float sc[4];              // their scales (column lane % 16)
 };
 
-template <bool GATEUP, int MT, bool NTB>
-__device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, int KC, int wv, int rows, int row0,
-                                          int nt, const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
-                                          int Ndim) {
+// KC chunks of 64 along A's rows; the weights have KCW chunks, and chunk c of A
+// meets weight chunk c % KCW (kChainF32 down: A = [hi | lo], KC = 2 * KCW).
+template <bool GATEUP, int MT, bool NTB, int CH>
+__device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, int KC, int KCW, int wv, int rows,
+                                          int row0, int nt, const uint16_t* __restrict__ src,
+                                          uint16_t* __restrict__ dst, int Ndim) {
   const int lane = threadIdx.x & 63;
   const uint32_t lds0 = lds_addr(smem);
   const uint8_t* const bring = smem + kGemmNA * kGemmA;
@@ -672,12 +725,13 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
   };
   auto issue_b = [&](int c) {
     const uint32_t st = lds0 + (uint32_t)(kGemmNA * kGemmA + (c % kGemmNB) * kGemmB + wv * 4096);
+    const int cw = c < KCW ? c : c - KCW;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       if (NTB)
-        dma16_stream(lane * 16, gl.bsrc[g] + c * 1024, st + g * 1024);
+        dma16_stream(lane * 16, gl.bsrc[g] + cw * 1024, st + g * 1024);
       else
-        dma16(lane * 16, gl.bsrc[g] + c * 1024, st + g * 1024);
+        dma16(lane * 16, gl.bsrc[g] + cw * 1024, st + g * 1024);
     }
   };
 
@@ -700,7 +754,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
     for (int g = 0; g < 4; ++g) raw[g] = *reinterpret_cast<const uint4*>(bp + g * 1024);
     bf16x8 lo[4], hi[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) dequant16(raw[g], gl.sc[g], lo[g], hi[g]);
+    for (int g = 0; g < 4; ++g) weights16<CH>(raw[g], gl.sc[g], lo[g], hi[g]);
     const uint16_t* As = reinterpret_cast<const uint16_t*>(smem + (c & 1) * kGemmA);
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -727,17 +781,26 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
     for (int j = 0; j < 4; ++j) {
       const int row = mi * 16 + 4 * (lane >> 4) + j;
       if (row >= rows) continue;
-      uint16_t* drow = dst + (size_t)(row0 + row) * Ndim;
+      uint16_t* drow = dst + (size_t)(row0 + row) * (GATEUP && CH == kChainF32 ? 2 * Ndim : Ndim);
       if (GATEUP) {
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          const float gv = round_bf16(acc[mi][g][j]);
-          const float uv = round_bf16(acc[mi][g + 2][j]);
-          drow[nt * 128 + wv * 32 + g * 16 + (lane & 15)] = f32_to_bf16_bits(silu_mul_fast(gv, uv));
+          const int col = nt * 128 + wv * 32 + g * 16 + (lane & 15);
+          if (CH == kChainAct) {
+            const float gv = round_bf16(acc[mi][g][j]);
+            const float uv = round_bf16(acc[mi][g + 2][j]);
+            drow[col] = f32_to_bf16_bits(swiglu<true>(gv, uv));
+          } else {
+            const float gv = __fmul_rn(acc[mi][g][j], gl.sc[g]);
+            const float uv = __fmul_rn(acc[mi][g + 2][j], gl.sc[g + 2]);
+            split_bf16(swiglu<false>(gv, uv), drow[col], drow[Ndim + col]);
+          }
         }
       } else {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) drow[nt * 256 + wv * 64 + g * 16 + (lane & 15)] = f32_to_bf16_bits(acc[mi][g][j]);
+        for (int g = 0; g < 4; ++g)
+          drow[nt * 256 + wv * 64 + g * 16 + (lane & 15)] =
+              f32_to_bf16_bits(CH == kChainF32 ? __fmul_rn(acc[mi][g][j], gl.sc[g]) : acc[mi][g][j]);
       }
     }
   }
@@ -748,7 +811,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
 // y_sorted. src must span fewer than 2^32 bytes (32-bit load offsets).
 // NTB: the weights are loaded with the nontemporal hint (few rows per expert,
 // so no second row tile would find them in L2).
-template <bool GATEUP, bool NTB>
+template <bool GATEUP, bool NTB, int CH>
 __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint16_t* __restrict__ src,
                                                   const int32_t* __restrict__ offsets,
                                                   const int32_t* __restrict__ sorted_token,
@@ -781,7 +844,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   __syncthreads();
 
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int Kdim = GATEUP ? D : I;
+  // kChainF32 down: A rows are h's hi and lo planes (2I wide)
+  const int Kdim = GATEUP ? D : (CH == kChainF32 ? 2 * I : I);
+  const int KCW = (GATEUP ? D : I) >> 6;
   const int Ndim = GATEUP ? I : D;
   GemmLoads gl;
   // A load j of wave wv covers tile rows 8q .. 8q+7, q = wv * 4 + j: lane -> (row, LDS piece lane % 8)
@@ -797,11 +862,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
     if (GATEUP) {
       const size_t cid = ((size_t)e * (I >> 4) + nt * 8 + 2 * wv + (g & 1)) * 2 + (g >> 1);
       gl.bsrc[g] = wp + cid * (size_t)(D >> 4) * 256;
-      gl.sc[g] = sp[cid * 16 + (lane & 15)];
+      gl.sc[g] = chain_scale<CH>(sp[cid * 16 + (lane & 15)]);
     } else {
       const size_t dg = (size_t)e * (D >> 4) + nt * 16 + 4 * wv + g;
       gl.bsrc[g] = wp + dg * (size_t)(I >> 4) * 256;
-      gl.sc[g] = sp[dg * 16 + (lane & 15)];
+      gl.sc[g] = chain_scale<CH>(sp[dg * 16 + (lane & 15)]);
     }
   }
   // consume the scale loads here, so the compiler's waits for them sit before
@@ -812,13 +877,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   const int KC = Kdim >> 6;
   const int nmt = (rows + 15) >> 4;
   if (nmt > 4)
-    gemm_tile<GATEUP, 8, NTB>(smem, gl, KC, wv, rows, row0, nt, src, dst, Ndim);
+    gemm_tile<GATEUP, 8, NTB, CH>(smem, gl, KC, KCW, wv, rows, row0, nt, src, dst, Ndim);
   else if (nmt > 2)
-    gemm_tile<GATEUP, 4, NTB>(smem, gl, KC, wv, rows, row0, nt, src, dst, Ndim);
+    gemm_tile<GATEUP, 4, NTB, CH>(smem, gl, KC, KCW, wv, rows, row0, nt, src, dst, Ndim);
   else if (nmt == 2)
-    gemm_tile<GATEUP, 2, NTB>(smem, gl, KC, wv, rows, row0, nt, src, dst, Ndim);
+    gemm_tile<GATEUP, 2, NTB, CH>(smem, gl, KC, KCW, wv, rows, row0, nt, src, dst, Ndim);
   else
-    gemm_tile<GATEUP, 1, NTB>(smem, gl, KC, wv, rows, row0, nt, src, dst, Ndim);
+    gemm_tile<GATEUP, 1, NTB, CH>(smem, gl, KC, KCW, wv, rows, row0, nt, src, dst, Ndim);
 }
 
 // ---------------------------------------------------------------------------
@@ -848,11 +913,21 @@ __device__ __forceinline__ float w_at(const WView& w, size_t idx, size_t sidx) {
   return BF16 ? round_bf16(q * round_bf16(sv)) : q * sv;
 }
 
-template <typename A>
+// kChainAct with bf16 activations rounds the weights and g, u, every silu step
+// and y to bf16; kChainF32 (and any chain with f32 activations) keeps weights
+// and intermediates in f32, h of bf16 activations as its hi and lo planes.
+template <typename A, int CH>
+struct GenericChain {
+  static constexpr bool kRound = Act<A>::kBf16 && CH == kChainAct;
+  static constexpr bool kSplitH = Act<A>::kBf16 && CH == kChainF32;
+};
+
+template <typename A, int CH>
 __global__ __launch_bounds__(256) void k_gateup_generic(int D, int I, const A* __restrict__ x,
                                                          const int32_t* __restrict__ sorted_token,
                                                          const int32_t* __restrict__ sorted_expert, WView wg, WView wu,
                                                          A* __restrict__ h_sorted) {
+  using C = GenericChain<A, CH>;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   const int m = blockIdx.y;
   if (i >= I) return;
@@ -861,33 +936,51 @@ __global__ __launch_bounds__(256) void k_gateup_generic(int D, int I, const A* _
   for (int d = 0; d < D; ++d) {
     const float xv = Act<A>::load(x, (int64_t)t * D + d);
     const size_t idx = ((size_t)e * D + d) * I + i;
-    g = __builtin_fmaf(xv, w_at<Act<A>::kBf16>(wg, idx, (size_t)e * I + i), g);
-    u = __builtin_fmaf(xv, w_at<Act<A>::kBf16>(wu, idx, (size_t)e * I + i), u);
+    g = __builtin_fmaf(xv, w_at<C::kRound>(wg, idx, (size_t)e * I + i), g);
+    u = __builtin_fmaf(xv, w_at<C::kRound>(wu, idx, (size_t)e * I + i), u);
   }
-  g = Act<A>::round(g);
-  u = Act<A>::round(u);
-  Act<A>::store(h_sorted, (int64_t)m * I + i, silu_f32(g) * u);
+  if (C::kRound) {
+    g = round_bf16(g);
+    u = round_bf16(u);
+  }
+  const float h = swiglu<C::kRound>(g, u);
+  if (C::kSplitH) {
+    uint16_t* hr = reinterpret_cast<uint16_t*>(h_sorted) + (int64_t)m * 2 * I + i;
+    split_bf16(h, hr[0], hr[I]);
+  } else {
+    Act<A>::store(h_sorted, (int64_t)m * I + i, h);
+  }
 }
 
-template <typename A>
+template <typename A, int CH>
 __global__ __launch_bounds__(256) void k_down_generic(int D, int I, const A* __restrict__ h_sorted,
                                                        const int32_t* __restrict__ sorted_expert, WView wd,
                                                        A* __restrict__ y_sorted) {
+  using C = GenericChain<A, CH>;
   const int n = blockIdx.x * blockDim.x + threadIdx.x;
   const int m = blockIdx.y;
   if (n >= D) return;
   const int e = sorted_expert[m];
   float acc = 0.0f;
   for (int i = 0; i < I; ++i) {
-    const float hv = Act<A>::load(h_sorted, (int64_t)m * I + i);
-    acc = __builtin_fmaf(hv, w_at<Act<A>::kBf16>(wd, ((size_t)e * I + i) * D + n, (size_t)e * D + n), acc);
+    float hv;
+    if (C::kSplitH) {
+      const uint16_t* hr = reinterpret_cast<const uint16_t*>(h_sorted) + (int64_t)m * 2 * I + i;
+      hv = bf16_bits_to_f32(hr[0]) + bf16_bits_to_f32(hr[I]);  // exact in f32
+    } else {
+      hv = Act<A>::load(h_sorted, (int64_t)m * I + i);
+    }
+    acc = __builtin_fmaf(hv, w_at<C::kRound>(wd, ((size_t)e * I + i) * D + n, (size_t)e * D + n), acc);
   }
   Act<A>::store(y_sorted, (int64_t)m * D + n, acc);
 }
 
 // ---------------------------------------------------------------------------
-// Combine: out[t, n] = round(sum_{j<K} w[t,j] * y_sorted[inv[t*K+j], n]),
-// sequential fmaf over j from +0.0f; no atomics, one writer per element.
+// Combine: out[t, n] from the terms p_j = round(w[t,j] * y_sorted[inv[t*K+j], n])
+// in j order: SCATTER = false sums them in f32 from +0.0f and rounds once
+// (jnp.sum of y_k * w, kappa/qwen3/ffn_moe.py:103); SCATTER = true rounds the
+// running sum after every add (out.at[token].add(y * w) into a zero buffer of
+// x.dtype, :157, :215). No atomics, one writer per element.
 // A thread owns 8 consecutive columns (one 16-byte bf16 load per row); the
 // row indices and weights of a token are read first and the K row loads are
 // issued in batches of 8 before the FMAs. With res (the residual stream h of
@@ -931,7 +1024,14 @@ struct Vec8<float> {
   }
 };
 
-template <typename A>
+// acc + round(w * y), the sum rounded again when SCATTER
+template <typename A, bool SCATTER>
+__device__ __forceinline__ float combine_term(float acc, float w, float y) {
+  const float s = __fadd_rn(acc, Act<A>::round(__fmul_rn(w, y)));
+  return SCATTER ? Act<A>::round(s) : s;
+}
+
+template <typename A, bool SCATTER>
 __global__ __launch_bounds__(256) void k_combine8(int T, int K, int D, const A* __restrict__ y,
                                                    const int32_t* __restrict__ inv, const float* __restrict__ w,
                                                    A* __restrict__ out, const A* __restrict__ res) {
@@ -959,7 +1059,7 @@ __global__ __launch_bounds__(256) void k_combine8(int T, int K, int D, const A* 
     for (int j = 0; j < 8; ++j)
       if (on[j])
 #pragma unroll
-        for (int v = 0; v < 8; ++v) acc[v] = __builtin_fmaf(wj[j], yv[j][v], acc[v]);
+        for (int v = 0; v < 8; ++v) acc[v] = combine_term<A, SCATTER>(acc[v], wj[j], yv[j][v]);
   }
   if (res) {
     // the block's output is rounded to the activation dtype, then added to h
@@ -972,7 +1072,7 @@ __global__ __launch_bounds__(256) void k_combine8(int T, int K, int D, const A* 
 }
 
 // Any D: one column per thread.
-template <typename A>
+template <typename A, bool SCATTER>
 __global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* __restrict__ y,
                                                    const int32_t* __restrict__ inv, const float* __restrict__ w,
                                                    A* __restrict__ out, const A* __restrict__ res) {
@@ -982,7 +1082,7 @@ __global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* 
   float acc = 0.0f;
   for (int j = 0; j < K; ++j) {
     const int p = inv[(int64_t)t * K + j];
-    if (p >= 0) acc = __builtin_fmaf(w[(int64_t)t * K + j], Act<A>::load(y, (int64_t)p * D + n), acc);
+    if (p >= 0) acc = combine_term<A, SCATTER>(acc, w[(int64_t)t * K + j], Act<A>::load(y, (int64_t)p * D + n));
   }
   if (res) acc = Act<A>::load(res, (int64_t)t * D + n) + Act<A>::round(acc);
   Act<A>::store(out, (int64_t)t * D + n, acc);
@@ -1005,7 +1105,7 @@ __global__ __launch_bounds__(256) void k_combine1(int T, int K, int D, const A* 
 // of several blocks is read by each of them, which is why the fused form stops
 // at 32 assignments (at 64 it was slower than the two kernels).
 // ---------------------------------------------------------------------------
-template <int KCMAX>
+template <int KCMAX, int CH, bool SCATTER>
 __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, int D, int I,
                                                         const uint16_t* __restrict__ h_sorted,
                                                         const int32_t* __restrict__ topk_idx,
@@ -1013,8 +1113,11 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, in
                                                         const float* __restrict__ topk_w,
                                                         const int8_t* __restrict__ w2, const float* __restrict__ s2,
                                                         uint16_t* __restrict__ out, const uint16_t* __restrict__ res) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t hrows[];  // [TPB*K][I]
+  // kChainF32: an h row is its hi and lo planes (2I)
+  constexpr int NP = CH == kChainF32 ? 2 : 1;
+  extern __shared__ __attribute__((aligned(16))) uint16_t hrows[];  // [TPB*K][NP*I]
   __shared__ float part[3][kDownCombineMaxRows][16];                // chains 0+1, 2, 3 of row 0
+  __shared__ float scl[kDownCombineMaxRows][16];                    // kChainF32: the column scales
   const int dt = blockIdx.x, tid = threadIdx.x;
   const int lane = tid & 63, wv = tid >> 6;  // blockDim.x = 128 * TPB * K
   const int m = wv >> 1, half = wv & 1;
@@ -1045,11 +1148,15 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, in
 #pragma unroll
     for (int c = 0; c < KCMAX; ++c)
       if (cl + c < ch) q[c] = load_stream16(bp + (size_t)(cl + c) * 1024);
-    const float sc = s2[(size_t)e * D + dt * 16 + (lane & 15)];
-    // this wave's chunks of the h row (8 pieces of 16 bytes per chunk)
-    uint16_t* hr = hrows + (size_t)m * I;
-    const uint4* src = reinterpret_cast<const uint4*>(h_sorted + (size_t)p * I);
-    for (int i = cl * 8 + lane; i < ch * 8; i += 64) reinterpret_cast<uint4*>(hr)[i] = src[i];
+    const float sc = chain_scale<CH>(s2[(size_t)e * D + dt * 16 + (lane & 15)]);
+    if (CH == kChainF32 && half == 0 && lane < 16) scl[m][lane] = sc;
+    // this wave's chunks of the h row (8 pieces of 16 bytes per chunk, per plane)
+    uint16_t* hr = hrows + (size_t)m * NP * I;
+    const uint4* src = reinterpret_cast<const uint4*>(h_sorted + (size_t)p * NP * I);
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl)
+      for (int i = cl * 8 + lane; i < ch * 8; i += 64)
+        reinterpret_cast<uint4*>(hr)[pl * (I >> 3) + i] = src[pl * (I >> 3) + i];
     // the pieces are read back by other lanes of this wave only
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1065,16 +1172,20 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, in
 #pragma unroll
       for (int c = 0; c < KCMAX; ++c) {
         if (cl + c >= c0 && cl + c < c1) {
-          uint4 a0v = uint4{0, 0, 0, 0}, a1v = uint4{0, 0, 0, 0};
-          if (row0) {
-            const uint4* ap = reinterpret_cast<const uint4*>(hr + (cl + c) * 64 + koff);
-            a0v = ap[0];
-            a1v = ap[1];
-          }
           bf16x8 b0, b1;
-          dequant16(q[c], sc, b0, b1);
-          acc[rr] = mfma16(as_bf16x8(a0v), b0, acc[rr]);
-          acc[rr] = mfma16(as_bf16x8(a1v), b1, acc[rr]);
+          weights16<CH>(q[c], sc, b0, b1);
+          // the planes in k_down_decode's order: hi then lo
+#pragma unroll
+          for (int pl = 0; pl < NP; ++pl) {
+            uint4 a0v = uint4{0, 0, 0, 0}, a1v = uint4{0, 0, 0, 0};
+            if (row0) {
+              const uint4* ap = reinterpret_cast<const uint4*>(hr + pl * I + (cl + c) * 64 + koff);
+              a0v = ap[0];
+              a1v = ap[1];
+            }
+            acc[rr] = mfma16(as_bf16x8(a0v), b0, acc[rr]);
+            acc[rr] = mfma16(as_bf16x8(a1v), b1, acc[rr]);
+          }
         }
       }
     }
@@ -1097,8 +1208,9 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, in
       // a dropped assignment (inv < 0, fixed_capacity) adds nothing
       if (j < K && cinv[j] >= 0) {
         const int mj = t * K + j;
-        const float y = round_bf16((part[0][mj][col] + part[1][mj][col]) + part[2][mj][col]);
-        acc = __builtin_fmaf(cw[j], y, acc);
+        float v = (part[0][mj][col] + part[1][mj][col]) + part[2][mj][col];
+        if (CH == kChainF32) v = __fmul_rn(v, scl[mj][col]);
+        acc = combine_term<uint16_t, SCATTER>(acc, cw[j], round_bf16(v));
       }
     }
     const int64_t o = (int64_t)(t0 + t) * D + dt * 16 + col;
@@ -1119,22 +1231,19 @@ namespace kmoe_host {
 
 using namespace kmoe;
 
-hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, const void* x, const int32_t* offsets,
-                                const int32_t* active, const int32_t* sorted_token, const kmoe_packed_experts& p,
-                                void* h_sorted, void* y_sorted, hipStream_t st) {
+namespace {
+
+// The packed-weight kernels of one rounding chain.
+template <int CH>
+hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint16_t* xb, const int32_t* offsets,
+                         const int32_t* active, const int32_t* sorted_token, const int8_t* w13, const float* s13,
+                         const int8_t* w2, const float* s2, uint16_t* hb, uint16_t* yb, hipStream_t st) {
   const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts, K = (int)d.top_k,
             I = (int)d.intermediate;
   const int M = T * K;
   const int slots = M < E ? M : E;
   const int cap = capacity_of(d);
-  const uint16_t* xb = reinterpret_cast<const uint16_t*>(x);
-  uint16_t* hb = reinterpret_cast<uint16_t*>(h_sorted);
-  uint16_t* yb = reinterpret_cast<uint16_t*>(y_sorted);
-  const int8_t* w13 = reinterpret_cast<const int8_t*>(p.w13);
-  const int8_t* w2 = reinterpret_cast<const int8_t*>(p.w2);
-  const float* s13 = reinterpret_cast<const float*>(p.s13);
-  const float* s2 = reinterpret_cast<const float*>(p.s2);
-  if (decode) {
+  if (family == kFamilyDecode) {
     // shapes from a sweep on MI355X (30B-A3B layer, T = 1..64): four waves split
     // the reduction, batches of 4 (gate/up) or 3 (down) chunks per load stage
     if (stages & kStageGateUp) {
@@ -1146,23 +1255,23 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
         // (DENSE); beyond, gathering only the expert's rows reads less.
         const bool dense = T <= 4;
         if (D / 64 == 32 && dense)
-          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, true, false>), grid, dim3(512), 0, st, T, D, I, E, xb, offsets,
-                             active, sorted_token, w13, s13, hb, cap);
+          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, true, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
+                             xb, offsets, active, sorted_token, w13, s13, hb, cap);
         else if (D / 64 == 32)
-          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, false, false>), grid, dim3(512), 0, st, T, D, I, E, xb,
-                             offsets, active, sorted_token, w13, s13, hb, cap);
+          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, false, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
+                             xb, offsets, active, sorted_token, w13, s13, hb, cap);
         else if (dense)
-          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, true, false>), grid, dim3(512), 0, st, T, D, I, E, xb, offsets,
-                             active, sorted_token, w13, s13, hb, cap);
+          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, true, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
+                             xb, offsets, active, sorted_token, w13, s13, hb, cap);
         else
-          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, false, false>), grid, dim3(512), 0, st, T, D, I, E, xb,
-                             offsets, active, sorted_token, w13, s13, hb, cap);
+          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, false, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
+                             xb, offsets, active, sorted_token, w13, s13, hb, cap);
       } else if ((D / 64) % 16 == 0) {
-        hipLaunchKernelGGL((k_gateup_decode<4, 4, false, kDecodeMaxRowBlocks, false, false>), grid, dim3(256), 0, st, T, D,
-                           I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
+        hipLaunchKernelGGL((k_gateup_decode<4, 4, false, kDecodeMaxRowBlocks, false, false, CH>), grid, dim3(256), 0,
+                           st, T, D, I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
       } else {
-        hipLaunchKernelGGL((k_gateup_decode<4, 4, true, kDecodeMaxRowBlocks, false, false>), grid, dim3(256), 0, st, T, D, I,
-                           E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
+        hipLaunchKernelGGL((k_gateup_decode<4, 4, true, kDecodeMaxRowBlocks, false, false, CH>), grid, dim3(256), 0,
+                           st, T, D, I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
       }
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
@@ -1171,16 +1280,17 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
       const int cpw = (I / 64) / 4;
       const dim3 grid(D / 32, slots);
       if ((I / 64) % 4 == 0 && cpw % 3 == 0)
-        hipLaunchKernelGGL((k_down_decode<4, 2, 3, false, false>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
-                           s2, yb, cap);
+        hipLaunchKernelGGL((k_down_decode<4, 2, 3, false, false, CH>), grid, dim3(256), 0, st, D, I, E, hb, offsets,
+                           active, w2, s2, yb, cap);
       else
-        hipLaunchKernelGGL((k_down_decode<4, 2, 4, true, false>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active, w2,
-                           s2, yb, cap);
+        hipLaunchKernelGGL((k_down_decode<4, 2, 4, true, false, CH>), grid, dim3(256), 0, st, D, I, E, hb, offsets,
+                           active, w2, s2, yb, cap);
       return hipGetLastError();
     }
     return hipSuccess;
   }
-  if (T <= kRowsPathMaxTokens && (D / 64 == 32 || D / 64 == 64) && (I / 64 == 12 || I / 64 == 24)) {
+  if (family == kFamilyRows && T <= kRowsPathMaxTokens && (D / 64 == 32 || D / 64 == 64) &&
+      (I / 64 == 12 || I / 64 == 24)) {
     // just above the decode sizes: the decode kernels over all of an expert's
     // rows in groups of 64, each wave's weights loaded once and kept in
     // registers (65 and 128 tokens: 158 -> 143 and 161 -> 155 us per layer
@@ -1188,28 +1298,29 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
     if (stages & kStageGateUp) {
       const dim3 grid(I / 16, slots);
       if (D / 64 == 32)
-        hipLaunchKernelGGL((k_gateup_decode<4, 8, false, kDecodeMaxRowBlocks, false, true>), grid, dim3(256), 0, st, T,
-                           D, I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
+        hipLaunchKernelGGL((k_gateup_decode<4, 8, false, kDecodeMaxRowBlocks, false, true, CH>), grid, dim3(256), 0,
+                           st, T, D, I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
       else
-        hipLaunchKernelGGL((k_gateup_decode<8, 8, false, kDecodeMaxRowBlocks, false, true>), grid, dim3(512), 0, st, T,
-                           D, I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
+        hipLaunchKernelGGL((k_gateup_decode<8, 8, false, kDecodeMaxRowBlocks, false, true, CH>), grid, dim3(512), 0,
+                           st, T, D, I, E, xb, offsets, active, sorted_token, w13, s13, hb, cap);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
     }
     if (stages & kStageDown) {
       const dim3 grid(D / 32, slots);
       if (I / 64 == 12)
-        hipLaunchKernelGGL((k_down_decode<4, 2, 3, false, true>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active,
-                           w2, s2, yb, cap);
+        hipLaunchKernelGGL((k_down_decode<4, 2, 3, false, true, CH>), grid, dim3(256), 0, st, D, I, E, hb, offsets,
+                           active, w2, s2, yb, cap);
       else
-        hipLaunchKernelGGL((k_down_decode<4, 2, 6, false, true>), grid, dim3(256), 0, st, D, I, E, hb, offsets, active,
-                           w2, s2, yb, cap);
+        hipLaunchKernelGGL((k_down_decode<4, 2, 6, false, true, CH>), grid, dim3(256), 0, st, D, I, E, hb, offsets,
+                           active, w2, s2, yb, cap);
       return hipGetLastError();
     }
     return hipSuccess;
   }
   // 32-bit load offsets: the gathered source must span fewer than 2^32 bytes
-  const bool small_src = (uint64_t)T * D * 2 < (1ull << 32) && (uint64_t)M * I * 2 < (1ull << 32);
+  const uint64_t hrow = CH == kChainF32 ? 2ull * I : (uint64_t)I;
+  const bool small_src = (uint64_t)T * D * 2 < (1ull << 32) && (uint64_t)M * hrow * 2 < (1ull << 32);
   if (I % 128 == 0 && D % 256 == 0 && small_src) {
     const int upper_mt = (M + kGemmRows - 1) / kGemmRows + slots;
     auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };
@@ -1220,21 +1331,21 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
     const bool ntb = M <= E * kGemmRows / 2;
     if (stages & kStageGateUp) {
       if (ntb)
-        hipLaunchKernelGGL((k_gemm<true, true>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb, offsets,
+        hipLaunchKernelGGL((k_gemm<true, true, CH>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb, offsets,
                            sorted_token, w13, s13, hb, cap);
       else
-        hipLaunchKernelGGL((k_gemm<true, false>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb, offsets,
-                           sorted_token, w13, s13, hb, cap);
+        hipLaunchKernelGGL((k_gemm<true, false, CH>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
+                           offsets, sorted_token, w13, s13, hb, cap);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
     }
     if (stages & kStageDown) {
       if (ntb)
-        hipLaunchKernelGGL((k_gemm<false, true>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb, offsets,
+        hipLaunchKernelGGL((k_gemm<false, true, CH>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb, offsets,
                            sorted_token, w2, s2, yb, cap);
       else
-        hipLaunchKernelGGL((k_gemm<false, false>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb, offsets,
-                           sorted_token, w2, s2, yb, cap);
+        hipLaunchKernelGGL((k_gemm<false, false, CH>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
+                           offsets, sorted_token, w2, s2, yb, cap);
       return hipGetLastError();
     }
     return hipSuccess;
@@ -1245,17 +1356,35 @@ hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, con
     return ((g + 7) / 8) * 8;
   };
   if (stages & kStageGateUp) {
-    hipLaunchKernelGGL((k_prefill<true>), dim3(grid_for(I / 64)), dim3(256), 0, st, D, I, E, xb, offsets,
+    hipLaunchKernelGGL((k_prefill<true, CH>), dim3(grid_for(I / 64)), dim3(256), 0, st, D, I, E, xb, offsets,
                        sorted_token, w13, s13, hb, cap);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   if (stages & kStageDown) {
-    hipLaunchKernelGGL((k_prefill<false>), dim3(grid_for(D / 128)), dim3(256), 0, st, D, I, E, hb, offsets,
+    hipLaunchKernelGGL((k_prefill<false, CH>), dim3(grid_for(D / 128)), dim3(256), 0, st, D, I, E, hb, offsets,
                        sorted_token, w2, s2, yb, cap);
     return hipGetLastError();
   }
   return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_expert_packed(const kmoe_desc& d, int chain, int family, int stages, const void* x,
+                                const int32_t* offsets, const int32_t* active, const int32_t* sorted_token,
+                                const kmoe_packed_experts& p, void* h_sorted, void* y_sorted, hipStream_t st) {
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(x);
+  uint16_t* hb = reinterpret_cast<uint16_t*>(h_sorted);
+  uint16_t* yb = reinterpret_cast<uint16_t*>(y_sorted);
+  const int8_t* w13 = reinterpret_cast<const int8_t*>(p.w13);
+  const int8_t* w2 = reinterpret_cast<const int8_t*>(p.w2);
+  const float* s13 = reinterpret_cast<const float*>(p.s13);
+  const float* s2 = reinterpret_cast<const float*>(p.s2);
+  if (chain == kChainF32)
+    return packed_stages<kChainF32>(d, family, stages, xb, offsets, active, sorted_token, w13, s13, w2, s2, hb, yb,
+                                    st);
+  return packed_stages<kChainAct>(d, family, stages, xb, offsets, active, sorted_token, w13, s13, w2, s2, hb, yb, st);
 }
 
 static WView make_view(const kmoe_weight& w) {
@@ -1268,26 +1397,26 @@ static WView make_view(const kmoe_weight& w) {
   return v;
 }
 
-template <typename A>
+template <typename A, int CH>
 static hipError_t generic_stages(int stages, int D, int I, int M, const void* x, const int32_t* sorted_token,
                                  const int32_t* sorted_expert, const WView& wg, const WView& wu, const WView& wd,
                                  void* h_sorted, void* y_sorted, hipStream_t st) {
   if (stages & kStageGateUp) {
-    hipLaunchKernelGGL((k_gateup_generic<A>), dim3((I + 255) / 256, M), dim3(256), 0, st, D, I,
+    hipLaunchKernelGGL((k_gateup_generic<A, CH>), dim3((I + 255) / 256, M), dim3(256), 0, st, D, I,
                        reinterpret_cast<const A*>(x), sorted_token, sorted_expert, wg, wu,
                        reinterpret_cast<A*>(h_sorted));
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   if (stages & kStageDown) {
-    hipLaunchKernelGGL((k_down_generic<A>), dim3((D + 255) / 256, M), dim3(256), 0, st, D, I,
+    hipLaunchKernelGGL((k_down_generic<A, CH>), dim3((D + 255) / 256, M), dim3(256), 0, st, D, I,
                        reinterpret_cast<const A*>(h_sorted), sorted_expert, wd, reinterpret_cast<A*>(y_sorted));
     return hipGetLastError();
   }
   return hipSuccess;
 }
 
-hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, const int32_t* sorted_token,
+hipError_t launch_expert_generic(const kmoe_desc& d, int chain, int stages, const void* x, const int32_t* sorted_token,
                                  const int32_t* sorted_expert, const kmoe_weight* gate, const kmoe_weight* up,
                                  const kmoe_weight* down, void* h_sorted, void* y_sorted, hipStream_t st) {
   const int T = (int)d.tokens, D = (int)d.hidden, K = (int)d.top_k, I = (int)d.intermediate;
@@ -1295,65 +1424,107 @@ hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, 
   const WView none = {nullptr, nullptr, 0, 0, 0};
   const WView wg = gate ? make_view(*gate) : none, wu = up ? make_view(*up) : none,
               wd = down ? make_view(*down) : none;
-  if (d.act_dtype == KMOE_DTYPE_BF16)
-    return generic_stages<uint16_t>(stages, D, I, M, x, sorted_token, sorted_expert, wg, wu, wd, h_sorted, y_sorted,
-                                    st);
-  return generic_stages<float>(stages, D, I, M, x, sorted_token, sorted_expert, wg, wu, wd, h_sorted, y_sorted, st);
+  if (d.act_dtype == KMOE_DTYPE_BF16) {
+    if (chain == kChainF32)
+      return generic_stages<uint16_t, kChainF32>(stages, D, I, M, x, sorted_token, sorted_expert, wg, wu, wd,
+                                                 h_sorted, y_sorted, st);
+    return generic_stages<uint16_t, kChainAct>(stages, D, I, M, x, sorted_token, sorted_expert, wg, wu, wd, h_sorted,
+                                               y_sorted, st);
+  }
+  // f32 activations: every chain computes in f32
+  return generic_stages<float, kChainF32>(stages, D, I, M, x, sorted_token, sorted_expert, wg, wu, wd, h_sorted,
+                                          y_sorted, st);
 }
 
-hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
-                          hipStream_t st, const void* res) {
+template <typename A, bool SCATTER>
+static void combine_launch(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w,
+                           void* out, hipStream_t st, const void* res) {
   const int T = (int)d.tokens, D = (int)d.hidden, K = (int)d.top_k;
-  const bool bf16 = d.act_dtype == KMOE_DTYPE_BF16;
-  if (D % 8 == 0) {
-    const dim3 grid((D / 8 + 255) / 256, T);
-    if (bf16)
-      hipLaunchKernelGGL((k_combine8<uint16_t>), grid, dim3(256), 0, st, T, K, D,
-                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out),
-                         reinterpret_cast<const uint16_t*>(res));
+  const A* y = reinterpret_cast<const A*>(y_sorted);
+  A* o = reinterpret_cast<A*>(out);
+  const A* r = reinterpret_cast<const A*>(res);
+  if (D % 8 == 0)
+    hipLaunchKernelGGL((k_combine8<A, SCATTER>), dim3((D / 8 + 255) / 256, T), dim3(256), 0, st, T, K, D, y, inv,
+                       topk_w, o, r);
+  else
+    hipLaunchKernelGGL((k_combine1<A, SCATTER>), dim3((D + 255) / 256, T), dim3(256), 0, st, T, K, D, y, inv, topk_w,
+                       o, r);
+}
+
+hipError_t launch_combine(const kmoe_desc& d, bool scatter, const void* y_sorted, const int32_t* inv,
+                          const float* topk_w, void* out, hipStream_t st, const void* res) {
+  if (d.act_dtype == KMOE_DTYPE_BF16) {
+    if (scatter)
+      combine_launch<uint16_t, true>(d, y_sorted, inv, topk_w, out, st, res);
     else
-      hipLaunchKernelGGL((k_combine8<float>), grid, dim3(256), 0, st, T, K, D, reinterpret_cast<const float*>(y_sorted),
-                         inv, topk_w, reinterpret_cast<float*>(out), reinterpret_cast<const float*>(res));
+      combine_launch<uint16_t, false>(d, y_sorted, inv, topk_w, out, st, res);
   } else {
-    const dim3 grid((D + 255) / 256, T);
-    if (bf16)
-      hipLaunchKernelGGL((k_combine1<uint16_t>), grid, dim3(256), 0, st, T, K, D,
-                         reinterpret_cast<const uint16_t*>(y_sorted), inv, topk_w, reinterpret_cast<uint16_t*>(out),
-                         reinterpret_cast<const uint16_t*>(res));
-    else
-      hipLaunchKernelGGL((k_combine1<float>), grid, dim3(256), 0, st, T, K, D, reinterpret_cast<const float*>(y_sorted),
-                         inv, topk_w, reinterpret_cast<float*>(out), reinterpret_cast<const float*>(res));
+    // f32: a rounded running sum is the f32 sum
+    combine_launch<float, false>(d, y_sorted, inv, topk_w, out, st, res);
   }
   return hipGetLastError();
 }
 
 // the weights of a wave's chunks (half the reduction) stay in registers: at
 // most 12 chunks of 64; a block holds the 8 / K tokens of up to 8 assignments
-bool down_combine_fits(const kmoe_desc& d) {
+// and their h rows (both planes for kChainF32) in LDS
+bool down_combine_fits(const kmoe_desc& d, int chain) {
   const int64_t M = d.tokens * d.top_k, KC = d.intermediate / 64;
+  const int64_t planes = chain == kChainF32 ? 2 : 1;
   return d.top_k >= 1 && d.top_k <= kDownCombineMaxRows && M <= kDownCombineMaxAssignments && KC <= 24 &&
-         (int64_t)kDownCombineMaxRows * d.intermediate * 2 <= 65536;
+         (int64_t)kDownCombineMaxRows * planes * d.intermediate * 2 <= 65536;
 }
 
-hipError_t launch_down_combine(const kmoe_desc& d, const void* h_sorted, const int32_t* topk_idx, const int32_t* inv,
-                               const float* topk_w, const kmoe_packed_experts& p, void* out, hipStream_t st,
-                               const void* res) {
+template <int KCMAX, int CH, bool SCATTER>
+static void down_combine_launch(dim3 grid, dim3 block, size_t lds, hipStream_t st, int T, int K, int TPB, int D,
+                                int I, const uint16_t* hb, const int32_t* topk_idx, const int32_t* inv,
+                                const float* topk_w, const int8_t* w2, const float* s2, uint16_t* ob,
+                                const uint16_t* rb) {
+  hipLaunchKernelGGL((k_down_combine<KCMAX, CH, SCATTER>), grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv,
+                     topk_w, w2, s2, ob, rb);
+}
+
+template <int KCMAX>
+static void down_combine_modes(int chain, bool scatter, dim3 grid, dim3 block, size_t lds, hipStream_t st, int T,
+                               int K, int TPB, int D, int I, const uint16_t* hb, const int32_t* topk_idx,
+                               const int32_t* inv, const float* topk_w, const int8_t* w2, const float* s2,
+                               uint16_t* ob, const uint16_t* rb) {
+  if (chain == kChainF32) {
+    if (scatter)
+      down_combine_launch<KCMAX, kChainF32, true>(grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w,
+                                                  w2, s2, ob, rb);
+    else
+      down_combine_launch<KCMAX, kChainF32, false>(grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w,
+                                                   w2, s2, ob, rb);
+  } else {
+    if (scatter)
+      down_combine_launch<KCMAX, kChainAct, true>(grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w,
+                                                  w2, s2, ob, rb);
+    else
+      down_combine_launch<KCMAX, kChainAct, false>(grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w,
+                                                   w2, s2, ob, rb);
+  }
+}
+
+hipError_t launch_down_combine(const kmoe_desc& d, int chain, bool scatter, const void* h_sorted,
+                               const int32_t* topk_idx, const int32_t* inv, const float* topk_w,
+                               const kmoe_packed_experts& p, void* out, hipStream_t st, const void* res) {
   const int T = (int)d.tokens, K = (int)d.top_k, D = (int)d.hidden, I = (int)d.intermediate;
-  if (!down_combine_fits(d)) return hipErrorInvalidValue;
+  if (!down_combine_fits(d, chain)) return hipErrorInvalidValue;
   const int TPB = std::min(T, kDownCombineMaxRows / K);
   const dim3 grid(D / 16, (T + TPB - 1) / TPB), block(128 * TPB * K);
-  const size_t lds = (size_t)TPB * K * I * 2;
+  const size_t lds = (size_t)TPB * K * I * 2 * (chain == kChainF32 ? 2 : 1);
   const uint16_t* hb = reinterpret_cast<const uint16_t*>(h_sorted);
   const int8_t* w2 = reinterpret_cast<const int8_t*>(p.w2);
   const float* s2 = reinterpret_cast<const float*>(p.s2);
   uint16_t* ob = reinterpret_cast<uint16_t*>(out);
   const uint16_t* rb = reinterpret_cast<const uint16_t*>(res);
   if (I / 64 <= 12)
-    hipLaunchKernelGGL((k_down_combine<6>), grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w, w2, s2,
-                       ob, rb);
+    down_combine_modes<6>(chain, scatter, grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w, w2, s2,
+                          ob, rb);
   else
-    hipLaunchKernelGGL((k_down_combine<12>), grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w, w2, s2,
-                       ob, rb);
+    down_combine_modes<12>(chain, scatter, grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w, w2, s2,
+                           ob, rb);
   return hipGetLastError();
 }
 

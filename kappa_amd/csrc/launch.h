@@ -50,25 +50,35 @@ hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const in
 // Stage selection bits for the expert launchers.
 constexpr int kStageGateUp = 1;  // x -> h_sorted (gate/up products + SwiGLU)
 constexpr int kStageDown = 2;    // h_sorted -> y_sorted (down product)
-// Packed int8 experts on MFMA; decode=true selects the small-T kernels.
-hipError_t launch_expert_packed(const kmoe_desc& d, bool decode, int stages, const void* x, const int32_t* offsets,
-                                const int32_t* active, const int32_t* sorted_token, const kmoe_packed_experts& p,
-                                void* h_sorted, void* y_sorted, hipStream_t st);
+// Kernel families of the packed experts: the GEMV-style decode kernels (T <= 64),
+// their row-group form (T <= 128, the 30B and 235B shapes; others fall back to
+// the GEMMs), the grouped GEMMs.
+constexpr int kFamilyDecode = 0;
+constexpr int kFamilyRows = 1;
+constexpr int kFamilyGemm = 2;
+// chain: kmoe::kChainAct or kmoe::kChainF32 (common.h); with kChainF32 and bf16
+// activations h_sorted holds [T*K][2I] bf16 (the hi and lo planes of h).
+// Packed int8 experts on MFMA.
+hipError_t launch_expert_packed(const kmoe_desc& d, int chain, int family, int stages, const void* x,
+                                const int32_t* offsets, const int32_t* active, const int32_t* sorted_token,
+                                const kmoe_packed_experts& p, void* h_sorted, void* y_sorted, hipStream_t st);
 // Layout-native experts (any weight kind), one sequential fmaf chain per output.
-hipError_t launch_expert_generic(const kmoe_desc& d, int stages, const void* x, const int32_t* sorted_token,
+hipError_t launch_expert_generic(const kmoe_desc& d, int chain, int stages, const void* x, const int32_t* sorted_token,
                                  const int32_t* sorted_expert, const kmoe_weight* gate, const kmoe_weight* up,
                                  const kmoe_weight* down, void* h_sorted, void* y_sorted, hipStream_t st);
-// out = round(sum_j w * y_sorted[inv]) [+ residual res, rounded again], res may be NULL
-hipError_t launch_combine(const kmoe_desc& d, const void* y_sorted, const int32_t* inv, const float* topk_w, void* out,
-                          hipStream_t st, const void* res = nullptr);
+// out = the terms round(w * y_sorted[inv]) summed in f32 and rounded once
+// (scatter = false) or added into a rounded running sum (scatter = true)
+// [+ residual res, rounded again], res may be NULL
+hipError_t launch_combine(const kmoe_desc& d, bool scatter, const void* y_sorted, const int32_t* inv,
+                          const float* topk_w, void* out, hipStream_t st, const void* res = nullptr);
 // Packed decode with T * K <= 32 and K <= 8 (down_combine_fits): the down
 // projection and the combine (with residual res, may be NULL) in one kernel;
 // out is bit-identical to the packed decode down kernel followed by
 // launch_combine.
-bool down_combine_fits(const kmoe_desc& d);
-hipError_t launch_down_combine(const kmoe_desc& d, const void* h_sorted, const int32_t* topk_idx, const int32_t* inv,
-                               const float* topk_w, const kmoe_packed_experts& p, void* out, hipStream_t st,
-                               const void* res);
+bool down_combine_fits(const kmoe_desc& d, int chain);
+hipError_t launch_down_combine(const kmoe_desc& d, int chain, bool scatter, const void* h_sorted,
+                               const int32_t* topk_idx, const int32_t* inv, const float* topk_w,
+                               const kmoe_packed_experts& p, void* out, hipStream_t st, const void* res);
 hipError_t launch_topk_w_cast(const kmoe_desc& d, const float* topk_w, void* out, hipStream_t st);
 
 // block.hip

@@ -53,8 +53,10 @@ __global__ __launch_bounds__(256) void k_pack_w2(int64_t ncell, int D, int I, co
   *reinterpret_cast<uint4*>(w2 + c * 16) = uint4{w[0], w[1], w[2], w[3]};
 }
 
-// s13 [E][I/16][2][16] and s2 [E][D]: scales rounded to bf16 (the scale is cast
-// to the compute dtype before the multiply, kappa/qwen3/quant.py:37).
+// s13 [E][I/16][2][16] and s2 [E][D]: the scales as given, in f32 (the kernels
+// cast them to bf16 for the gather and fixed_capacity programs,
+// kappa/qwen3/quant.py:37, and use them as they are for the ragged program's
+// f32 dequantisation, kappa/qwen3/ffn_moe.py:203-205).
 __global__ __launch_bounds__(256) void k_pack_scales(int E, int D, int I, const void* __restrict__ gs, int g_bf16,
                                                      int g_pc, const void* __restrict__ us, int u_bf16, int u_pc,
                                                      const void* __restrict__ ds, int d_bf16, int d_pc,
@@ -69,10 +71,10 @@ __global__ __launch_bounds__(256) void k_pack_scales(int E, int D, int I, const 
     const int64_t e = r / (I >> 4);
     const int64_t ch = e * I + ig * 16 + col;
     const float v = which ? scale_at(us, u_bf16, u_pc ? ch : 0) : scale_at(gs, g_bf16, g_pc ? ch : 0);
-    s13[i] = round_bf16(v);
+    s13[i] = v;
   } else if (i < n13 + (int64_t)E * D) {
     const int64_t j = i - n13;
-    s2[j] = round_bf16(scale_at(ds, d_bf16, d_pc ? j : 0));
+    s2[j] = scale_at(ds, d_bf16, d_pc ? j : 0);
   }
 }
 

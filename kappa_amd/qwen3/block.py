@@ -18,16 +18,7 @@ import torch
 
 from .. import _lib
 from .architecture import Qwen3Config
-from .ffn_moe import (
-    _MOE_IMPLS,
-    PackedExperts,
-    _desc,
-    _effective_moe_impl,
-    _fixed_capacity,
-    _moe_forward,
-    _norm_scale,
-    _stream,
-)
+from .ffn_moe import PackedExperts, _desc, _impl_and_capacity, _moe_forward, _norm_scale, _stream
 from .quant import Weight, kmoe_dtype
 
 
@@ -48,7 +39,7 @@ def rms_norm(
     xf = x.reshape(T, d).contiguous()
     sc = _norm_scale(scale, d, x.device)
     out = torch.empty((T, d), dtype=x.dtype, device=x.device)
-    desc = _desc(T, d, 1, 1, 1, x.dtype, 0)
+    desc = _desc(T, d, 1, 1, 1, x.dtype)
     _lib.check(
         _lib.lib().kmoe_rms_norm(
             desc, xf.data_ptr(), sc.data_ptr(), kmoe_dtype(sc.dtype), float(epsilon), out.data_ptr(), _stream(x.device)
@@ -75,17 +66,10 @@ def moe_block_ffn(
     if not cfg.use_moe:
         raise ValueError("moe_swiglu_ffn requires cfg.use_moe")
     b, t = int(h.shape[0]), int(h.shape[1])
-    impl = _effective_moe_impl(cfg, total_tokens=b * t)
-    if impl not in _MOE_IMPLS:
-        raise ValueError(f"unknown moe_impl: {impl!r}")
-    capacity = 0
-    if impl == "fixed_capacity":
-        if cfg.moe_capacity_factor <= 0:
-            raise ValueError("fixed_capacity requires cfg.moe_capacity_factor > 0")
-        capacity = _fixed_capacity(cfg, b * t)
+    impl, capacity = _impl_and_capacity(cfg, b * t)
     return _moe_forward(
         h, router_w, ffn_gate, ffn_up, ffn_down,
-        num_experts=cfg.num_experts, num_experts_per_tok=cfg.num_experts_per_tok,
+        num_experts=cfg.num_experts, num_experts_per_tok=cfg.num_experts_per_tok, impl=impl,
         decode_threshold=cfg.moe_ragged_decode_token_threshold, packed=packed, capacity=capacity,
         norm=(pre_ffn_norm, epsilon),
     )  # fmt: skip

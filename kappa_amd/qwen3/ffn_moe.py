@@ -7,17 +7,30 @@ are plain tensors or ``Q8Weight``. The block runs entirely in libkmoe.so:
 
   router logits -> top-k + softmax -> dispatch sort -> SwiGLU experts -> combine
 
-W8 experts with bf16 activations are relaid out once (``prepack_moe_experts``)
-for the MFMA kernels; the packed copy is cached per weight tensor so repeated
-calls with the same weights do not repack. ``T <= cfg.moe_ragged_decode_token_threshold``
-selects the decode kernels (the reference's decode switch, kappa/qwen3/ffn_moe.py:219-223);
-every kernel family follows the same numerics, so the choice only affects speed.
+Each ``cfg.moe_impl`` keeps its own rounding points, as the reference's array
+programs write them: ``gather_einsum`` (the default, and what ``ragged_jax`` /
+``ragged_tokamax`` run at ``T <= cfg.moe_ragged_decode_token_threshold``,
+kappa/qwen3/ffn_moe.py:219-223) computes the expert products in x.dtype and sums
+the rounded weighted terms in f32; ``ragged_*`` above the threshold computes
+them in f32 and adds the rounded terms into an x.dtype buffer; ``fixed_capacity``
+drops assignments beyond each expert's slot limit, computes in x.dtype and adds
+like the ragged path. The gather program takes per-tensor scales only
+(kappa/qwen3/quant.py:71-74), so per-output-channel W8 weights run with
+``ragged_*`` (a threshold of 0 for decode batches) or ``fixed_capacity``.
+
+The kernel family (GEMV-style up to 64 tokens, grouped GEMMs above) is chosen
+by token count, independently of the impl; the families follow the same
+rounding points but add the f32 products in different orders, so they agree
+to rounding, not bit for bit. W8 experts with bf16 activations are relaid out
+once for the MFMA kernels: ``prepack_moe_experts`` at load time (pass the result
+as ``packed=``), or implicitly through a cache keyed by the weight tensors.
 """
 
 from __future__ import annotations
 
 import math
 import threading
+import weakref
 from collections import OrderedDict
 from dataclasses import dataclass
 
@@ -26,9 +39,16 @@ import torch
 
 from .. import _lib
 from .architecture import Qwen3Config
-from .quant import Q8Weight, Weight, is_q8_weight, kmoe_dtype, weight_struct
+from .quant import Q8Weight, Weight, is_q8_weight, kmoe_dtype, scale_kind, weight_struct
 
 _MOE_IMPLS = ("gather_einsum", "fixed_capacity", "ragged_jax", "ragged_tokamax")
+# kmoe_impl of each MoEImpl (kappa/qwen3/architecture.py:14)
+_IMPL_CODE = {
+    "gather_einsum": _lib.IMPL_GATHER_EINSUM,
+    "fixed_capacity": _lib.IMPL_FIXED_CAPACITY,
+    "ragged_jax": _lib.IMPL_RAGGED,
+    "ragged_tokamax": _lib.IMPL_RAGGED,
+}
 
 # Upper bound on B*T when deriving the static fixed_capacity buffer depth
 # (kappa/qwen3/ffn_moe.py:20).
@@ -83,16 +103,21 @@ class PackedExperts:
     hidden: int
     intermediate: int
     num_experts: int
+    source_scale_kind: int  # _lib.SCALE_TENSOR or _lib.SCALE_CHANNEL
 
     def struct(self) -> _lib.KmoePacked:
-        return _lib.KmoePacked(self.w13.data_ptr(), self.s13.data_ptr(), self.w2.data_ptr(), self.s2.data_ptr())
+        return _lib.KmoePacked(
+            self.w13.data_ptr(), self.s13.data_ptr(), self.w2.data_ptr(), self.s2.data_ptr(), self.num_experts,
+            self.hidden, self.intermediate, self.source_scale_kind,
+        )  # fmt: skip
 
 
 def _desc(
-    T: int, D: int, E: int, K: int, I: int, act: torch.dtype, threshold: int, capacity: int = 0
+    T: int, D: int, E: int, K: int, I: int, act: torch.dtype, *, impl: str = "gather_einsum", threshold: int = 64,
+    capacity: int = 0, kernels: int = _lib.KERNELS_AUTO,
 ) -> _lib.KmoeDesc:
-    """kmoe_desc; capacity 0 is dropless, > 0 the fixed_capacity slot limit."""
-    return _lib.KmoeDesc(T, D, E, K, I, kmoe_dtype(act), threshold, capacity)
+    """kmoe_desc for the MoEImpl ``impl`` (capacity: the fixed_capacity slot limit)."""
+    return _lib.KmoeDesc(T, D, E, K, I, kmoe_dtype(act), _IMPL_CODE[impl], threshold, capacity, kernels)
 
 
 def _stream(device: torch.device) -> int:
@@ -107,8 +132,19 @@ def packable(x_dtype: torch.dtype, gate: Weight, up: Weight, down: Weight) -> bo
     return D % 64 == 0 and I % 64 == 0
 
 
+def _source_scale_kind(ws, n_outs, E) -> int:
+    kinds = [scale_kind(w, n, E) for w, n in zip(ws, n_outs)]
+    return _lib.SCALE_TENSOR if all(k == _lib.SCALE_TENSOR for k in kinds) else _lib.SCALE_CHANNEL
+
+
 def prepack_moe_experts(ffn_gate: Q8Weight, ffn_up: Q8Weight, ffn_down: Q8Weight) -> PackedExperts:
-    """One-time relayout of W8 experts ([E,D,I], [E,D,I], [E,I,D]) for the MFMA kernels."""
+    """One-time relayout of W8 experts ([E,D,I], [E,D,I], [E,I,D]) for the MFMA kernels.
+
+    The load-time step: run it once per layer when the weights are loaded (next to
+    the reference's quantize_qwen3_params, kappa/qwen3/weights.py:143-188) and pass
+    the result to ``moe_swiglu_ffn(..., packed=)``. The packed copy holds the same
+    int8 values and the scales as given; it does not follow later in-place writes
+    to the source tensors."""
     E, D, I = _shape(ffn_gate)
     if _shape(ffn_up) != (E, D, I) or _shape(ffn_down) != (E, I, D):
         raise ValueError(
@@ -119,7 +155,7 @@ def prepack_moe_experts(ffn_gate: Q8Weight, ffn_up: Q8Weight, ffn_down: Q8Weight
     g, kg = weight_struct(ffn_gate, dev, n_out=I, n_groups=E, name="ffn_gate")
     u, ku = weight_struct(ffn_up, dev, n_out=I, n_groups=E, name="ffn_up")
     d, kd = weight_struct(ffn_down, dev, n_out=D, n_groups=E, name="ffn_down")
-    desc = _desc(0, D, E, 1, I, torch.bfloat16, 0)
+    desc = _desc(0, D, E, 1, I, torch.bfloat16)
     sizes = _lib.KmoePackedSizes()
     L = _lib.lib()
     _lib.check(L.kmoe_prepack_bytes(desc, sizes))
@@ -127,43 +163,69 @@ def prepack_moe_experts(ffn_gate: Q8Weight, ffn_up: Q8Weight, ffn_down: Q8Weight
     s13 = torch.empty(sizes.s13_bytes // 4, dtype=torch.float32, device=dev)
     w2 = torch.empty(sizes.w2_bytes, dtype=torch.int8, device=dev)
     s2 = torch.empty(sizes.s2_bytes // 4, dtype=torch.float32, device=dev)
-    packed = PackedExperts(w13, s13, w2, s2, D, I, E)
+    kind = _source_scale_kind((ffn_gate, ffn_up, ffn_down), (I, I, D), E)
+    packed = PackedExperts(w13, s13, w2, s2, D, I, E, kind)
     _lib.check(L.kmoe_prepack(desc, g, u, d, packed.struct(), _stream(dev)))
     return packed
 
 
 class _PackCache:
-    """Small LRU of packed experts keyed by the source tensors' storage and version."""
+    """Packed experts for weights passed without ``packed=``, keyed by the source tensors.
 
-    def __init__(self, capacity: int = 4):
-        self.capacity = capacity
+    An entry lives as long as all of its source tensors (values and scales of
+    gate, up and down): it holds only weak references to them and is dropped when
+    any of them is freed, so a new tensor that reuses a freed address can never
+    hit an old entry. A hit also requires every source's ``_version`` to be
+    unchanged (torch in-place ops). ``max_entries`` bounds the count (least
+    recently used first out); the default holds every MoE layer of the largest
+    Qwen3 models."""
+
+    def __init__(self, max_entries: int = 256):
+        self.max_entries = max_entries
         self._d: OrderedDict = OrderedDict()
-        self._lock = threading.Lock()
+        self._lock = threading.RLock()
+        self.packs = 0  # prepack calls made (a miss)
 
     @staticmethod
-    def key(*ws: Q8Weight) -> tuple:
-        parts = []
+    def _sources(ws) -> tuple[list, tuple]:
+        """The source tensors, and the values of scales given as Python numbers."""
+        src, scalars = [], []
         for w in ws:
             for t in (w.values, w.scale):
                 if isinstance(t, torch.Tensor):
-                    parts.append((t.data_ptr(), t._version, tuple(t.shape), t.dtype, t.device))
+                    src.append(t)
                 else:
-                    parts.append(("scalar", float(t)))
-        return tuple(parts)
+                    scalars.append(float(t))
+        return src, tuple(scalars)
+
+    def _evict(self, key) -> None:
+        with self._lock:
+            self._d.pop(key, None)
 
     def get(self, gate: Q8Weight, up: Q8Weight, down: Q8Weight) -> PackedExperts:
-        k = self.key(gate, up, down)
+        src, scalars = self._sources((gate, up, down))
+        key = tuple(id(t) for t in src) + scalars
+        stamp = tuple((t._version, t.data_ptr()) for t in src)
         with self._lock:
-            hit = self._d.get(k)
-            if hit is not None:
-                self._d.move_to_end(k)
-                return hit
+            ent = self._d.get(key)
+            if ent is not None:
+                refs, st, packed = ent
+                if all(r() is t for r, t in zip(refs, src)) and st == stamp:
+                    self._d.move_to_end(key)
+                    return packed
+                del self._d[key]
         packed = prepack_moe_experts(gate, up, down)
         with self._lock:
-            self._d[k] = packed
-            while len(self._d) > self.capacity:
+            self.packs += 1
+            self._d[key] = ([weakref.ref(t) for t in src], stamp, packed)
+            for t in src:
+                weakref.finalize(t, self._evict, key)
+            while len(self._d) > self.max_entries:
                 self._d.popitem(last=False)
         return packed
+
+    def __len__(self) -> int:
+        return len(self._d)
 
     def clear(self) -> None:
         with self._lock:
@@ -209,6 +271,35 @@ def _norm_scale(scale: torch.Tensor, d: int, dev: torch.device) -> torch.Tensor:
     return scale.reshape(d).to(dev).contiguous()
 
 
+def _check_packed(packed: PackedExperts, E: int, d: int, I: int, dev: torch.device) -> None:
+    """A packed copy must hold this layer's shapes, on x's device."""
+    if not isinstance(packed, PackedExperts):
+        raise ValueError(f"packed must be a PackedExperts from prepack_moe_experts (got {type(packed).__name__})")
+    if (packed.num_experts, packed.hidden, packed.intermediate) != (E, d, I):
+        raise ValueError(
+            f"packed experts hold E={packed.num_experts}, D={packed.hidden}, I={packed.intermediate}; "
+            f"the layer has E={E}, D={d}, I={I}"
+        )
+    for name in ("w13", "s13", "w2", "s2"):
+        if getattr(packed, name).device != dev:
+            raise ValueError(f"packed.{name} is on {getattr(packed, name).device}, x is on {dev}")
+
+
+def _check_gather_scales(impl: str, ws, n_outs, E: int) -> None:
+    """The gather program (moe_take_dequant, kappa/qwen3/quant.py:71-74) multiplies the
+    gathered [T, K, D, I] values by the scale as stored: it takes a per-tensor scale
+    (or one expert's [1, 1, N]), not per-expert per-channel scales."""
+    if impl != "gather_einsum" or E <= 1:
+        return
+    for w, n in zip(ws, n_outs):
+        if is_q8_weight(w) and scale_kind(w, n, E) == _lib.SCALE_CHANNEL:
+            raise ValueError(
+                "gather_einsum takes one scale per tensor (kappa/qwen3/quant.py:71-74); per-channel scales run "
+                "with moe_impl='ragged_jax' / 'ragged_tokamax' (moe_ragged_decode_token_threshold=0 for decode "
+                "batches) or 'fixed_capacity'"
+            )
+
+
 def _moe_forward(
     x: torch.Tensor,
     router_w: Weight,
@@ -218,19 +309,18 @@ def _moe_forward(
     *,
     num_experts: int,
     num_experts_per_tok: int,
+    impl: str,
     decode_threshold: int,
     packed: PackedExperts | None,
     return_routing: bool = False,
     capacity: int = 0,
     norm: tuple[torch.Tensor, float] | None = None,
+    kernels: int = _lib.KERNELS_AUTO,
 ):
-    """The block through the C ABI. With ``norm = (scale, epsilon)``, ``x`` is the
+    """The block through the C ABI for the MoEImpl ``impl`` (the configured one; the
+    library applies the decode switch). With ``norm = (scale, epsilon)``, ``x`` is the
     residual stream h and the call returns h + block(rms_norm(h)) (kmoe_forward_block)."""
     b, t, d = _route_checks(x, router_w, num_experts)
-    if x.device.type != "cuda":
-        raise ValueError(f"x must be on a HIP device (got {x.device}); the block has no CPU implementation")
-    if x.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError(f"x must be bfloat16 or float32 (got {x.dtype})")
     E, K = num_experts, num_experts_per_tok
     if _expert_count(ffn_gate) != E:
         raise ValueError(f"ffn_gate has {_expert_count(ffn_gate)} experts, cfg.num_experts is {E}")
@@ -240,10 +330,20 @@ def _moe_forward(
             f"expert shapes gate {_shape(ffn_gate)}, up {_shape(ffn_up)}, down {_shape(ffn_down)} "
             f"do not match [E,D,I]/[E,I,D] with D={d}, E={E}"
         )
-    dev = x.device
     T = b * t
+    effective = _effective_moe_impl(
+        Qwen3ConfigView(impl, decode_threshold), total_tokens=T
+    )  # the program that runs (kappa/qwen3/ffn_moe.py:219-223)
+    _check_gather_scales(effective, (ffn_gate, ffn_up, ffn_down), (I, I, d), E)
+    dev = x.device
+    if packed is not None:
+        _check_packed(packed, E, d, I, dev)
+    if dev.type != "cuda":
+        raise ValueError(f"x must be on a HIP device (got {dev}); the block has no CPU implementation")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"x must be bfloat16 or float32 (got {x.dtype})")
     x_flat = x.reshape(T, d).contiguous()
-    desc = _desc(T, d, E, K, I, x.dtype, decode_threshold, capacity)
+    desc = _desc(T, d, E, K, I, x.dtype, impl=impl, threshold=decode_threshold, capacity=capacity, kernels=kernels)
     r, kr = weight_struct(router_w, dev, n_out=E, n_groups=None, name="router_w")
     if packed is None and packable(x.dtype, ffn_gate, ffn_up, ffn_down):
         packed = PACK_CACHE.get(ffn_gate, ffn_up, ffn_down)
@@ -281,6 +381,29 @@ def _moe_forward(
     return out
 
 
+@dataclass(frozen=True)
+class Qwen3ConfigView:
+    """The two Qwen3Config fields _effective_moe_impl reads."""
+
+    moe_impl: str
+    moe_ragged_decode_token_threshold: int
+
+
+def _impl_and_capacity(cfg: Qwen3Config, total_tokens: int) -> tuple[str, int]:
+    """The configured impl (validated, kappa/qwen3/ffn_moe.py:250-252, 299) and its slot limit."""
+    impl = cfg.moe_impl
+    if impl not in _MOE_IMPLS:
+        raise ValueError(f"unknown moe_impl: {impl!r}")
+    capacity = 0
+    if _effective_moe_impl(cfg, total_tokens=total_tokens) == "fixed_capacity":
+        if cfg.moe_capacity_factor <= 0:
+            raise ValueError("fixed_capacity requires cfg.moe_capacity_factor > 0")
+        # token dropping: each expert keeps its first `capacity` assignments in the
+        # stable (expert, token) order
+        capacity = _fixed_capacity(cfg, total_tokens)
+    return impl, capacity
+
+
 def moe_swiglu_ffn(
     x: torch.Tensor,
     router_w: Weight,
@@ -291,7 +414,8 @@ def moe_swiglu_ffn(
     cfg: Qwen3Config,
     packed: PackedExperts | None = None,
 ) -> torch.Tensor:
-    """MoE SwiGLU forward (kappa/qwen3/ffn_moe.py:226-299).
+    """MoE SwiGLU forward (kappa/qwen3/ffn_moe.py:226-299); implementation selected by
+    ``cfg.moe_impl`` (and the decode threshold).
 
     Shapes: ``router_w`` ``[D, E]``; ``ffn_*`` ``[E, D, I]`` / ``[E, I, D]`` for
     gate/up/down. Returns ``[B, T, D]`` in ``x.dtype``. ``packed`` optionally
@@ -301,20 +425,10 @@ def moe_swiglu_ffn(
         raise ValueError("moe_swiglu_ffn requires cfg.use_moe")
     _route_checks(x, router_w, cfg.num_experts)
     b, t = int(x.shape[0]), int(x.shape[1])
-    impl = _effective_moe_impl(cfg, total_tokens=b * t)
-    if impl not in _MOE_IMPLS:
-        raise ValueError(f"unknown moe_impl: {impl!r}")
-    capacity = 0
-    if impl == "fixed_capacity":
-        if cfg.moe_capacity_factor <= 0:
-            raise ValueError("fixed_capacity requires cfg.moe_capacity_factor > 0")
-        # token dropping: the dropless kernels with each expert limited to its
-        # first `capacity` assignments in the stable (expert, token) order
-        capacity = _fixed_capacity(cfg, b * t)
-    # gather_einsum, ragged_jax and ragged_tokamax are dropless and share one numerics contract here.
+    impl, capacity = _impl_and_capacity(cfg, b * t)
     return _moe_forward(
         x, router_w, ffn_gate, ffn_up, ffn_down,
-        num_experts=cfg.num_experts, num_experts_per_tok=cfg.num_experts_per_tok,
+        num_experts=cfg.num_experts, num_experts_per_tok=cfg.num_experts_per_tok, impl=impl,
         decode_threshold=cfg.moe_ragged_decode_token_threshold, packed=packed, capacity=capacity,
     )  # fmt: skip
 
@@ -329,9 +443,10 @@ def moe_swiglu_ffn_legacy(
     num_experts: int,
     num_experts_per_tok: int,
 ) -> torch.Tensor:
-    """Backward-compatible API with explicit expert counts (kappa/qwen3/ffn_moe.py:302-316)."""
+    """Backward-compatible API: always the gather program, whatever a config says
+    (kappa/qwen3/ffn_moe.py:302-316)."""
     return _moe_forward(
         x, router_w, ffn_gate, ffn_up, ffn_down,
-        num_experts=num_experts, num_experts_per_tok=num_experts_per_tok,
+        num_experts=num_experts, num_experts_per_tok=num_experts_per_tok, impl="gather_einsum",
         decode_threshold=64, packed=None,
     )  # fmt: skip

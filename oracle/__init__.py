@@ -17,10 +17,14 @@ Function -> reference it restates:
   router_logits   kappa/qwen3/ffn_moe.py:46-50   (_route logits)
   topk_softmax    kappa/qwen3/ffn_moe.py:51-55   (lax.top_k + softmax)
   dispatch        kappa/qwen3/ffn_moe.py:189-200, 212 (argsort stable, bincount, inv)
-  expert_ffn      kappa/qwen3/ffn_moe.py:99-102 with kappa/qwen3/quant.py:60-76
-  combine         kappa/qwen3/ffn_moe.py:103, 214-215
-  forward         kappa/qwen3/ffn_moe.py:226-299 (moe_swiglu_ffn; capacity= gives
-                  the fixed_capacity path, :107-158)
+  expert_ffn      impl "gather_einsum": kappa/qwen3/ffn_moe.py:87-102 with
+                  kappa/qwen3/quant.py:60-76; "fixed_capacity": :146-152;
+                  "ragged": :202-213 (ragged_jax and ragged_tokamax)
+  combine         "gather_einsum": :103; "ragged": :212-215; "fixed_capacity": :153-157
+  forward         kappa/qwen3/ffn_moe.py:226-299 (moe_swiglu_ffn for one impl,
+                  the one _effective_moe_impl, :219-223, selects; capacity= gives
+                  the fixed_capacity drops, :107-158)
+  effective_impl  kappa/qwen3/ffn_moe.py:219-223
   capacity_slots  kappa/qwen3/ffn_moe.py:23-31, 136-141 (c_buf and c_dyn)
   drop_over_capacity  kappa/qwen3/ffn_moe.py:59-71, 141, 153 (slot within expert, mask)
   quantize_*      kappa/qwen3/quant.py:41-48
@@ -69,12 +73,12 @@ def lib() -> ctypes.CDLL:
         L.orc_router_logits.argtypes = [_i64, _i64, _i64, _f32p, _f32p, _i8p, _f32p, _f32p]
         L.orc_topk_softmax.argtypes = [_i64, _i64, _i64, ctypes.c_int, _f32p, _i32p, _f32p]
         L.orc_dispatch.argtypes = [_i64, _i64, _i64, _i32p, _i32p, _i32p, _i32p, _i32p, _i32p]
-        L.orc_expert_ffn.argtypes = [_i64, _i64, _i64, _i64, _i64, ctypes.c_int, _f32p, _i32p, _i32p] + [
+        L.orc_expert_ffn.argtypes = [_i64, _i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _f32p, _i32p, _i32p] + [
             _f32p,
             _i8p,
             _f32p,
         ] * 3 + [_f32p, _f32p]
-        L.orc_combine.argtypes = [_i64, _i64, _i64, ctypes.c_int, _f32p, _i32p, _f32p, _f32p]
+        L.orc_combine.argtypes = [_i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _f32p, _i32p, _f32p, _f32p]
         L.orc_rms_norm.argtypes = [_i64, _i64, ctypes.c_int, _f32p, _f32p, ctypes.c_float, _f32p]
         L.orc_quantize_per_channel.argtypes = [_i64, _i64, _i64, _f32p, _i8p, _f32p]
         L.orc_quantize_per_tensor.restype = ctypes.c_float
@@ -161,8 +165,32 @@ def dispatch(idx, num_experts: int) -> dict:
     return {"group_sizes": gs, "offsets": off, "order": order, "sorted_token": st, "inv": inv}
 
 
-def expert_ffn(x, offsets, sorted_token, gate, up, down, act_bf16: bool):
-    """N4/N5: (h_sorted [M, I], y_sorted [M, D]) for the sorted assignment rows."""
+# The three array programs of the reference's MoE layer (kappa/qwen3/ffn_moe.py):
+# which rounding chain the expert products follow and how the combine adds.
+IMPLS = ("gather_einsum", "ragged", "fixed_capacity")
+_CHAIN = {"gather_einsum": 0, "fixed_capacity": 0, "ragged": 1}  # ORC_CHAIN_ACT / ORC_CHAIN_F32
+_COMBINE = {"gather_einsum": 0, "fixed_capacity": 1, "ragged": 1}  # ORC_COMBINE_SUM / ORC_COMBINE_SCATTER
+
+
+def _impl(impl: str) -> str:
+    if impl in ("ragged_jax", "ragged_tokamax"):
+        return "ragged"
+    if impl not in IMPLS:
+        raise ValueError(f"unknown impl {impl!r}; expected one of {IMPLS}")
+    return impl
+
+
+def effective_impl(moe_impl: str, total_tokens: int, threshold: int = 64) -> str:
+    """_effective_moe_impl (kappa/qwen3/ffn_moe.py:219-223), in the oracle's names."""
+    if moe_impl in ("ragged_jax", "ragged_tokamax"):
+        return "gather_einsum" if total_tokens <= threshold else "ragged"
+    return _impl(moe_impl)
+
+
+def expert_ffn(x, offsets, sorted_token, gate, up, down, act_bf16: bool, *, impl: str):
+    """(h_sorted [M, I], y_sorted [M, D]) for the sorted assignment rows, with the
+    rounding points of ``impl``'s expert products (h is f32 under "ragged")."""
+    chain = _CHAIN[_impl(impl)]
     x = _f32(x)
     T, D = x.shape
     offsets = np.ascontiguousarray(offsets, np.int32)
@@ -177,7 +205,7 @@ def expert_ffn(x, offsets, sorted_token, gate, up, down, act_bf16: bool):
     h = np.empty((M, I), np.float32)
     y = np.empty((M, D), np.float32)
     lib().orc_expert_ffn(
-        T, D, E, 0, I, int(act_bf16), _p(x, _f32p), _p(offsets, _i32p), _p(sorted_token, _i32p),
+        T, D, E, 0, I, int(act_bf16), chain, _p(x, _f32p), _p(offsets, _i32p), _p(sorted_token, _i32p),
         _p(gf, _f32p), _p(gq, _i8p), _p(gs, _f32p),
         _p(uf, _f32p), _p(uq, _i8p), _p(us, _f32p),
         _p(df, _f32p), _p(dq, _i8p), _p(ds, _f32p),
@@ -186,15 +214,18 @@ def expert_ffn(x, offsets, sorted_token, gate, up, down, act_bf16: bool):
     return h, y
 
 
-def combine(y_sorted, inv, w, act_bf16: bool) -> np.ndarray:
-    """N6: out [T, D] = round(sum_j w[t,j] * y_sorted[inv[t*K+j]])."""
+def combine(y_sorted, inv, w, act_bf16: bool, *, impl: str) -> np.ndarray:
+    """out [T, D] from y_sorted rows inv[t*K+j] and weights w [T, K] (inv < 0: dropped):
+    "gather_einsum" rounds each product and sums in f32 (:103); "ragged" and
+    "fixed_capacity" add the rounded products into a zero buffer of x.dtype (:156-157, :214-215)."""
+    mode = _COMBINE[_impl(impl)]
     y_sorted = _f32(y_sorted)
     w = _f32(w)
     inv = np.ascontiguousarray(inv, np.int32)
     T, K = w.shape
     D = y_sorted.shape[1]
     out = np.empty((T, D), np.float32)
-    lib().orc_combine(T, K, D, int(act_bf16), _p(y_sorted, _f32p), _p(inv, _i32p), _p(w, _f32p), _p(out, _f32p))
+    lib().orc_combine(T, K, D, int(act_bf16), mode, _p(y_sorted, _f32p), _p(inv, _i32p), _p(w, _f32p), _p(out, _f32p))
     return out
 
 
@@ -225,18 +256,22 @@ def drop_over_capacity(idx, disp: dict, capacity: int) -> np.ndarray:
     return inv
 
 
-def forward(x, router, gate, up, down, *, k: int, act_bf16: bool, capacity: int | None = None) -> dict:
-    """Whole block on flattened tokens x [T, D]; returns every intermediate.
+def forward(x, router, gate, up, down, *, k: int, act_bf16: bool, impl: str, capacity: int | None = None) -> dict:
+    """Whole block on flattened tokens x [T, D] with the array program ``impl``
+    ("gather_einsum", "ragged" or "fixed_capacity"); returns every intermediate.
 
-    capacity: None for the dropless paths, else the fixed_capacity slot limit."""
+    capacity: the fixed_capacity slot limit (impl "fixed_capacity" requires it)."""
+    impl = _impl(impl)
+    if (impl == "fixed_capacity") != (capacity is not None):
+        raise ValueError("capacity is given exactly when impl is fixed_capacity")
     logits = router_logits(x, router)
     E = logits.shape[1]
     idx, w = topk_softmax(logits, k, act_bf16)
     disp = dispatch(idx, E)
     if capacity is not None:
         disp["inv"] = drop_over_capacity(idx, disp, capacity)
-    h, y = expert_ffn(x, disp["offsets"], disp["sorted_token"], gate, up, down, act_bf16)
-    out = combine(y, disp["inv"], w, act_bf16)
+    h, y = expert_ffn(x, disp["offsets"], disp["sorted_token"], gate, up, down, act_bf16, impl=impl)
+    out = combine(y, disp["inv"], w, act_bf16, impl=impl)
     return {"logits": logits, "idx": idx, "w": w, **disp, "h_sorted": h, "y_sorted": y, "out": out}
 
 
@@ -259,10 +294,11 @@ def residual_add(h, moe_out, act_bf16: bool) -> np.ndarray:
     return bf16_round(s) if act_bf16 else s
 
 
-def forward_block(h, norm_scale, router, gate, up, down, *, k: int, act_bf16: bool, eps: float = 1e-6) -> dict:
+def forward_block(h, norm_scale, router, gate, up, down, *, k: int, act_bf16: bool, impl: str, eps: float = 1e-6,
+                  capacity: int | None = None) -> dict:
     """h + moe_swiglu_ffn(rms_norm(h, norm_scale)) (kappa/qwen3/block.py:196-207)."""
     h2 = rms_norm(h, norm_scale, eps, act_bf16)
-    moe = forward(h2, router, gate, up, down, k=k, act_bf16=act_bf16)
+    moe = forward(h2, router, gate, up, down, k=k, act_bf16=act_bf16, impl=impl, capacity=capacity)
     return {**moe, "h2": h2, "moe_out": moe["out"], "out": residual_add(h, moe["out"], act_bf16)}
 
 

@@ -8,30 +8,54 @@
  * It restates, in plain C, the arithmetic of the reference layer
  *   moe_swiglu_ffn(x, router_w, ffn_gate, ffn_up, ffn_down, *, cfg)
  *   (kappa/qwen3/ffn_moe.py:226-299)
- * under one numerics contract shared with the GPU kernels:
+ * following the rounding points each implementation of the reference writes
+ * down (kappa/qwen3/ffn_moe.py): the router is shared, the expert products and
+ * the combine depend on the MoEImpl that runs (after the decode switch of
+ * _effective_moe_impl, :219-223).
  *
- *  N0 logits[t,e] = sum_d f32(x[t,d]) * r[d,e]   (kappa/qwen3/ffn_moe.py:50)
+ * Router (_route, :38-56), every impl:
+ *  N0 logits[t,e] = sum_d f32(x[t,d]) * r[d,e]   (:50)
  *     in a canonical order: D is cut into slices of 64; each slice is a
  *     sequential fmaf chain starting from +0.0f; slice partials are combined
  *     by a pairwise tree (p[i] += p[i+s], s = 1,2,4,...), zero-padded to a
  *     power of two.  r = to_compute_dtype(router_w, f32)
- *     (kappa/qwen3/ffn_moe.py:46, kappa/qwen3/quant.py:34-38).
+ *     (:46, kappa/qwen3/quant.py:34-38).
  *  N1 top-k by value, descending, ties to the lower expert index
- *     (jax.lax.top_k, kappa/qwen3/ffn_moe.py:51).
- *  N2 w = round_act(softmax_f32(top_logits)) (kappa/qwen3/ffn_moe.py:52):
+ *     (jax.lax.top_k, :51).
+ *  N2 w = act(softmax_f32(top_logits)) (:52):
  *     e_j = expf(l_j - l_0), s = sum_j e_j in j order, w_j = e_j / s.
  *  N3 dispatch = stable sort of the row-major (t, j) assignment list by expert
- *     (jnp.argsort(stable=True), kappa/qwen3/ffn_moe.py:196-200, 212).
- *  N4 W8 dequant: bf16 activations: bf16(f32(q) * bf16(s)); f32 activations:
- *     f32(q) * f32(s) (kappa/qwen3/quant.py:37, :74 - the scale is cast to
- *     the compute dtype before the multiply).
- *  N5 g,u = round_act(sum_d x*W) (sequential fmaf over d from +0.0f),
- *     h = round_act(silu(g) * u) with silu(g) = g / (1 + expf(-g)),
- *     y_j = round_act(sum_i h*Wd) (kappa/qwen3/ffn_moe.py:99-102).
- *  N6 out[t] = round_act(sum_j w_j * y_j), sequential fmaf over j from +0.0f
- *     (kappa/qwen3/ffn_moe.py:103, :214-215).
- * round_act is the identity for f32 activations and round-to-nearest-even to
- * bfloat16 for bf16 activations. Every bf16 value is carried in a float.
+ *     (jnp.argsort(stable=True), :196-200, 212; jnp.lexsort((token, expert)),
+ *     :130, gives the same order).
+ *
+ * act(v) rounds to the activation dtype: the identity for f32 activations,
+ * round-to-nearest-even to bfloat16 for bf16 activations. Every bf16 value is
+ * carried in a float. Each jnp operation of the written program rounds its
+ * result to its array dtype; XLA may legally keep more precision inside a
+ * fusion, which no file of the reference pins.
+ *
+ * Expert products, ORC_CHAIN_ACT (gather_einsum :74-104 through
+ * moe_take_dequant, kappa/qwen3/quant.py:60-76; fixed_capacity :146-152
+ * through to_compute_dtype(., x.dtype)):
+ *  W = act(f32(q) * act(s))  (the scale cast to x.dtype first, quant.py:37,74)
+ *  g = act(sum_d x*W), u likewise (sequential fmaf over d from +0.0f)
+ *  h = act(act(g * act(sigmoid(g))) * u)   (jax.nn.silu(g) * u, :101, :151:
+ *      silu(g) = g * sigmoid(g), each op in x.dtype)
+ *  y = act(sum_i h*Wd)
+ * Expert products, ORC_CHAIN_F32 (_moe_ragged :202-213):
+ *  W = f32(q) * f32(s) in f32 (to_compute_dtype(., f32), :203-205)
+ *  g, u = sum_d f32(x)*W in f32; h = (g * sigmoid(g)) * u in f32 (:209)
+ *  y = act(sum_i h*Wd) (the f32 ragged_dot, then y.astype(x.dtype), :210-213)
+ * sigmoid(g) = 1 / (1 + expf(-g)) in f32.
+ *
+ * Combine, ORC_COMBINE_SUM (gather_einsum, :103):
+ *  p_j = act(y_j * w_j); out = act(sum_j f32(p_j)) summed in j order from
+ *  +0.0f (jnp.sum of a bf16 array accumulates in f32 and rounds once).
+ * Combine, ORC_COMBINE_SCATTER (_moe_ragged :214-215, fixed_capacity :156-157):
+ *  p_j = act(y_j * w_j); o = 0; o = act(o + p_j) for j = 0..K-1
+ *  (out_flat.at[token_flat].add in x.dtype: each update rounds; the updates
+ *  of token t arrive in j order). A dropped assignment (fixed_capacity,
+ *  y_pick = 0, :153) contributes act(0 * w) = 0 and is skipped.
  *
  * Around the block (the steps on either side of it in a Qwen3 MoE layer,
  * kappa/qwen3/block.py:196-207):
@@ -93,15 +117,23 @@ int orc_get_threads(void) {
 #endif
 }
 
+/* Expert-product chains and combines (see the header). */
+#define ORC_CHAIN_ACT 0
+#define ORC_CHAIN_F32 1
+#define ORC_COMBINE_SUM 0
+#define ORC_COMBINE_SCATTER 1
+
 /* One weight tensor [E][Kd][N]: either plain floats (wf != NULL) or int8
  * values wq with one f32 scale per (expert, output channel) ws[e*N + n].
  * A per-tensor scale is passed as a per-channel array with equal entries
- * (kappa/qwen3/quant.py:15-19 stores one scalar; broadcasting it is exact). */
+ * (kappa/qwen3/quant.py:15-19 stores one scalar; broadcasting it is exact).
+ * act_w: dequantise to the activation dtype (ORC_CHAIN_ACT with bf16
+ * activations, values.astype(bf16) * scale.astype(bf16)); otherwise to f32. */
 static inline float deq(const float* wf, const int8_t* wq, const float* ws, int64_t idx, int64_t sidx,
-                        int round_bf16) {
-  if (wf) return round_bf16 ? bf16r(wf[idx]) : wf[idx];
+                        int act_w) {
+  if (wf) return act_w ? bf16r(wf[idx]) : wf[idx];
   float q = (float)wq[idx];
-  if (round_bf16) return bf16r(q * bf16r(ws[sidx]));
+  if (act_w) return bf16r(q * bf16r(ws[sidx]));
   return q * ws[sidx];
 }
 
@@ -205,19 +237,36 @@ void orc_dispatch(int64_t T, int64_t K, int64_t E, const int32_t* idx, int32_t* 
   free(fill);
 }
 
-static inline float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+static inline float sigmoid_f32(float g) { return 1.0f / (1.0f + expf(-g)); }
 
-/* N4 + N5 over the sorted rows: h_sorted [M][I], y_sorted [M][D].
+/* h from g and u (jax.nn.silu(g) * u, kappa/qwen3/ffn_moe.py:101, 151, 209):
+ * silu(g) = g * sigmoid(g); every product rounded to act (ORC_CHAIN_ACT with
+ * bf16 activations) or to f32. */
+static inline float swiglu(float g, float u, int act) {
+  if (act) {
+    const float sg = bf16r(g * bf16r(sigmoid_f32(g)));
+    return bf16r(sg * u);
+  }
+  const float sg = g * sigmoid_f32(g);
+  return sg * u;
+}
+
+/* Expert products over the sorted rows: h_sorted [M][I], y_sorted [M][D].
  * Weights: gate/up [E][D][I], down [E][I][D] (kappa/qwen3/weights.py:58-62,
  * kappa/checkpoint/qwen_hf_convert.py:212-218); each is plain (f) or int8
- * values (q) with per-(expert, output channel) scales (s). */
+ * values (q) with per-(expert, output channel) scales (s).
+ * chain ORC_CHAIN_ACT: _moe_gather_einsum / _moe_fixed_capacity rounding
+ * points (kappa/qwen3/ffn_moe.py:99-102, 149-152); ORC_CHAIN_F32:
+ * _moe_ragged (:202-213). h_sorted holds f32 values under ORC_CHAIN_F32. */
 #define ORC_ROWS 4
-void orc_expert_ffn(int64_t T, int64_t D, int64_t E, int64_t K, int64_t I, int round_bf16, const float* x,
-                    const int32_t* offsets, const int32_t* sorted_token, const float* gf, const int8_t* gq,
-                    const float* gs, const float* uf, const int8_t* uq, const float* us, const float* df,
-                    const int8_t* dq, const float* ds, float* h_sorted, float* y_sorted) {
+void orc_expert_ffn(int64_t T, int64_t D, int64_t E, int64_t K, int64_t I, int round_bf16, int chain,
+                    const float* x, const int32_t* offsets, const int32_t* sorted_token, const float* gf,
+                    const int8_t* gq, const float* gs, const float* uf, const int8_t* uq, const float* us,
+                    const float* df, const int8_t* dq, const float* ds, float* h_sorted, float* y_sorted) {
   (void)T;
   (void)K;
+  /* the arrays that carry x.dtype in the written program */
+  const int act = round_bf16 && chain == ORC_CHAIN_ACT;
   int64_t nblocks_total = 0;
   for (int64_t e = 0; e < E; ++e) nblocks_total += (offsets[e + 1] - offsets[e] + ORC_ROWS - 1) / ORC_ROWS;
   /* flatten (expert, row block) pairs so that OpenMP balances skewed groups */
@@ -247,8 +296,8 @@ void orc_expert_ffn(int64_t T, int64_t D, int64_t E, int64_t K, int64_t I, int r
         float* wg = wrow;
         float* wu = wrow + I;
         for (int64_t i = 0; i < I; ++i) {
-          wg[i] = deq(gf, gq, gs, base + i, e * I + i, round_bf16);
-          wu[i] = deq(uf, uq, us, base + i, e * I + i, round_bf16);
+          wg[i] = deq(gf, gq, gs, base + i, e * I + i, act);
+          wu[i] = deq(uf, uq, us, base + i, e * I + i, act);
         }
         for (int64_t r = 0; r < nr; ++r) {
           float xv = x[(int64_t)sorted_token[m0 + r] * D + d];
@@ -264,19 +313,17 @@ void orc_expert_ffn(int64_t T, int64_t D, int64_t E, int64_t K, int64_t I, int r
         float* hr = h_sorted + (m0 + r) * I;
         for (int64_t i = 0; i < I; ++i) {
           float g = accg[r * I + i], u = accu[r * I + i];
-          if (round_bf16) {
+          if (act) {
             g = bf16r(g);
             u = bf16r(u);
-            hr[i] = bf16r(silu_f32(g) * u);
-          } else {
-            hr[i] = silu_f32(g) * u;
           }
+          hr[i] = swiglu(g, u, act);
         }
       }
       for (int64_t i = 0; i < ORC_ROWS * D; ++i) accy[i] = 0.0f;
       for (int64_t i = 0; i < I; ++i) {
         int64_t base = (e * I + i) * D;
-        for (int64_t n = 0; n < D; ++n) wrow[n] = deq(df, dq, ds, base + n, e * D + n, round_bf16);
+        for (int64_t n = 0; n < D; ++n) wrow[n] = deq(df, dq, ds, base + n, e * D + n, act);
         for (int64_t r = 0; r < nr; ++r) {
           float hv = h_sorted[(m0 + r) * I + i];
           float* ay = accy + r * D;
@@ -297,18 +344,22 @@ void orc_expert_ffn(int64_t T, int64_t D, int64_t E, int64_t K, int64_t I, int r
   free(blk_m);
 }
 
-/* N6: deterministic weighted combine back to token order. */
-void orc_combine(int64_t T, int64_t K, int64_t D, int round_bf16, const float* y_sorted, const int32_t* inv,
+/* Weighted combine back to token order (kappa/qwen3/ffn_moe.py:103 with
+ * ORC_COMBINE_SUM, :156-157 / :214-215 with ORC_COMBINE_SCATTER). inv < 0
+ * marks an assignment dropped by fixed_capacity (y_pick = 0, :153): its
+ * product is zero and it is skipped. */
+void orc_combine(int64_t T, int64_t K, int64_t D, int round_bf16, int mode, const float* y_sorted, const int32_t* inv,
                  const float* w, float* out) {
 #pragma omp parallel for schedule(static)
   for (int64_t t = 0; t < T; ++t) {
     for (int64_t n = 0; n < D; ++n) {
       float acc = 0.0f;
       for (int64_t j = 0; j < K; ++j) {
-        /* inv < 0: an assignment dropped by fixed_capacity adds nothing
-         * (kappa/qwen3/ffn_moe.py:153, y_pick = 0) */
         if (inv[t * K + j] < 0) continue;
-        acc = fmaf(w[t * K + j], y_sorted[(int64_t)inv[t * K + j] * D + n], acc);
+        float p = y_sorted[(int64_t)inv[t * K + j] * D + n] * w[t * K + j];
+        if (round_bf16) p = bf16r(p);
+        acc = acc + p;
+        if (mode == ORC_COMBINE_SCATTER && round_bf16) acc = bf16r(acc);
       }
       out[t * D + n] = round_bf16 ? bf16r(acc) : acc;
     }

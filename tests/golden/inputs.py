@@ -47,6 +47,10 @@ class Spec:
     x_zero: bool = False  # KAT: x = 0 gives all-equal logits
     tie_router: bool = False  # KAT: duplicated router columns give exact logit ties
     skew_lambda: float = 0.0  # Zipf(1.2) routing bias injected through x[:,0] and router[0,:]
+    # the reference array program the case follows: "gather_einsum"
+    # (kappa/qwen3/ffn_moe.py:74-104), "ragged" (:174-216, moe_impl ragged_jax /
+    # ragged_tokamax above the decode threshold) or "fixed_capacity" (:107-158)
+    impl: str = "gather_einsum"
     extra: dict = field(default_factory=dict)
 
     def as_dict(self) -> dict:
@@ -135,44 +139,64 @@ def digest(inputs: dict) -> str:
     return h.hexdigest()
 
 
-# Golden cases. Shapes follow the reference's own checks and the benchmark workloads:
-#   verify_f32:  scripts/verify_qwen3_moe_impls.py:23 (b=2,t=3,d=16,e=8,k=2,i=32, fp32)
-#   toy_f32:     the CPU-runnable toy block (T=64, D=256, E=8, K=2, I=128, fp32, N(0,0.02))
-#   w8c_*:       small W8 per-channel bf16 blocks (the 30B layer's numerics at toy size)
-#   w8t_bf16:    the reference's per-tensor Q8 with a bf16 scale (kappa/qwen3/quant.py:41)
-#   tie_*:       known-answer tests for the top-k tie rule
+# Golden cases. Shapes follow the reference's own checks and the benchmark workloads.
+# The gather path (moe_take_dequant, kappa/qwen3/quant.py:71-74) multiplies the
+# gathered [T, K, D, I] values by the scale as stored, so it takes a per-tensor
+# scale or plain weights; per-output-channel scales ([E, 1, N]) run on the
+# ragged path, whose to_compute_dtype broadcasts them (:203-205).
+#   verify_f32:   scripts/verify_qwen3_moe_impls.py:23 (b=2,t=3,d=16,e=8,k=2,i=32, fp32)
+#   toy_f32:      the CPU-runnable toy block (T=64, D=256, E=8, K=2, I=128, fp32, N(0,0.02))
+#   w8t_bf16:     the reference's per-tensor Q8 with a bf16 scale (kappa/qwen3/quant.py:41)
+#   g30_w8t:      the 30B-A3B per-token shape (D 2048, I 768, top-8) with per-tensor
+#                 bf16 scales, 16 experts, 8 tokens: the default decode program
+#   w8c_*:        small W8 per-channel bf16 blocks on the ragged path
+#   r30_w8c:      the 30B-A3B per-token shape with per-channel f32 scales, ragged
+#   r_*:          the ragged program on the other weight kinds (f32, per-tensor, bf16)
+#   tie_*:        known-answer tests for the top-k tie rule
 GOLDEN_SPECS = [
     Spec("verify_f32", T=6, D=16, E=8, K=2, I=32, act="f32", weights="f32", router="f32", x_std=1.0),
     Spec("toy_f32", T=64, D=256, E=8, K=2, I=128, act="f32", weights="f32", router="f32", x_std=0.02),
-    Spec("w8c_bf16", T=32, D=128, E=16, K=4, I=64),
-    Spec("w8c_bf16_k8", T=24, D=192, E=32, K=8, I=96, base_seed=10),
     Spec("w8t_bf16", T=16, D=128, E=8, K=2, I=64, weights="w8t", scale_dtype="bf16", base_seed=20),
-    Spec("w8c_qrouter", T=16, D=128, E=8, K=2, I=64, router="w8t", scale_dtype="bf16", base_seed=30),
     Spec("bf16_plain", T=16, D=128, E=8, K=2, I=64, weights="bf16", base_seed=40),
-    Spec("tie_zero_x", T=4, D=64, E=8, K=3, I=32, x_zero=True, base_seed=50),
-    Spec("tie_router", T=8, D=64, E=8, K=3, I=32, tie_router=True, base_seed=60),
+    Spec("g30_w8t", T=8, D=2048, E=16, K=8, I=768, weights="w8t", scale_dtype="bf16", base_seed=200),
+    Spec("tie_router", T=8, D=64, E=8, K=3, I=32, weights="w8t", scale_dtype="bf16", tie_router=True, base_seed=60),
+    Spec("w8c_bf16", T=32, D=128, E=16, K=4, I=64, impl="ragged"),
+    Spec("w8c_bf16_k8", T=24, D=192, E=32, K=8, I=96, base_seed=10, impl="ragged"),
+    Spec("w8c_qrouter", T=16, D=128, E=8, K=2, I=64, router="w8t", scale_dtype="bf16", base_seed=30, impl="ragged"),
+    Spec("r30_w8c", T=16, D=2048, E=16, K=8, I=768, base_seed=210, impl="ragged"),
+    Spec("r_toy_f32", T=64, D=256, E=8, K=2, I=128, act="f32", weights="f32", router="f32", x_std=0.02,
+         base_seed=220, impl="ragged"),  # fmt: skip
+    Spec("r_w8t_bf16", T=16, D=128, E=8, K=2, I=64, weights="w8t", scale_dtype="bf16", base_seed=230, impl="ragged"),
+    Spec("r_bf16_plain", T=16, D=128, E=8, K=2, I=64, weights="bf16", base_seed=240, impl="ragged"),
+    Spec("tie_zero_x", T=4, D=64, E=8, K=3, I=32, x_zero=True, base_seed=50, impl="ragged"),
 ]
 
 # fixed_capacity cases (kappa/qwen3/ffn_moe.py:107-158): (spec, capacity_factor, moe_fixed_capacity_slots)
 #   cap_w8c_bf16:   c_dyn = round(0.5 * 128 / 16) = 4 slots for ~8 assignments per expert
 #   cap_f32_slots:  c_dyn = round(1.25 * 48 / 8) = 8, capped by 3 static slots (c_buf)
 #   cap_skew_bf16:  Zipf-skewed routing, c_dyn = 6: the hot experts overflow
+#   cap30_w8c:      the 30B-A3B per-token shape, c_dyn = round(0.5 * 128 / 16) = 4
 CAPACITY_SPECS = [
-    (Spec("cap_w8c_bf16", T=32, D=128, E=16, K=4, I=64, base_seed=70), 0.5, None),
-    (Spec("cap_f32_slots", T=24, D=64, E=8, K=2, I=32, act="f32", weights="f32", router="f32", base_seed=80), 1.25, 3),
-    (Spec("cap_skew_bf16", T=48, D=128, E=16, K=2, I=64, skew_lambda=1.0, base_seed=90), 1.0, None),
+    (Spec("cap_w8c_bf16", T=32, D=128, E=16, K=4, I=64, base_seed=70, impl="fixed_capacity"), 0.5, None),
+    (Spec("cap_f32_slots", T=24, D=64, E=8, K=2, I=32, act="f32", weights="f32", router="f32", base_seed=80,
+          impl="fixed_capacity"), 1.25, 3),  # fmt: skip
+    (Spec("cap_skew_bf16", T=48, D=128, E=16, K=2, I=64, skew_lambda=1.0, base_seed=90, impl="fixed_capacity"), 1.0,
+     None),  # fmt: skip
+    (Spec("cap30_w8c", T=16, D=2048, E=16, K=8, I=768, base_seed=250, impl="fixed_capacity"), 0.5, None),
 ]
 
 
 # The MoE block with the steps either side of it (kappa/qwen3/block.py:196-207):
 # (spec, epsilon). The spec's x is the residual stream h; the RMSNorm scale
 # (pre_ffn_norm, seed 7) is N(1, 0.1), rounded to bf16 for bf16 activations.
-#   blk_w8c_bf16:  the 30B numerics at toy size
-#   blk_d192_k8:   hidden 192 (three slices: a zero-padded sum tree), top-8
-#   blk_toy_f32:   the fp32 toy block
+#   blk_w8c_bf16:  the 30B numerics at toy size (ragged)
+#   blk_d192_k8:   hidden 192 (three slices: a zero-padded sum tree), top-8 (ragged)
+#   blk_w8t_bf16:  per-tensor scales on the gather path
+#   blk_toy_f32:   the fp32 toy block (gather)
 BLOCK_SPECS = [
-    (Spec("blk_w8c_bf16", T=32, D=128, E=16, K=4, I=64, base_seed=100), 1e-6),
-    (Spec("blk_d192_k8", T=24, D=192, E=32, K=8, I=96, base_seed=110), 1e-5),
+    (Spec("blk_w8c_bf16", T=32, D=128, E=16, K=4, I=64, base_seed=100, impl="ragged"), 1e-6),
+    (Spec("blk_d192_k8", T=24, D=192, E=32, K=8, I=96, base_seed=110, impl="ragged"), 1e-5),
+    (Spec("blk_w8t_bf16", T=16, D=128, E=8, K=2, I=64, weights="w8t", scale_dtype="bf16", base_seed=130), 1e-6),
     (Spec("blk_toy_f32", T=16, D=256, E=8, K=2, I=128, act="f32", weights="f32", router="f32", base_seed=120), 1e-6),
 ]
 

@@ -2,8 +2,15 @@
 
 Big layers (the 30B-A3B and 235B-A22B shapes) are generated on the device:
 weights ~ N(0, 0.02) from a seeded torch generator, quantised per output
-channel by the library's quantiser, activations bf16 ~ N(0, 1), router bf16 ~
-N(0, 0.02). Host copies (numpy) feed the oracle.
+channel by the library's quantiser (or per tensor with a bf16 scale, the
+reference's own quantize_weight, kappa/qwen3/quant.py:41-48), activations bf16
+~ N(0, 1), router bf16 ~ N(0, 0.02). Host copies (numpy) feed the oracle.
+
+Each layer call names the reference array program it is checked against:
+per-channel layers run the ragged program (moe_impl ragged_jax with a decode
+threshold of 0 at every token count, as scripts/verify_qwen3_moe_impls.py:51
+configures it, or the default threshold above 64 tokens) or fixed_capacity;
+per-tensor layers also run the gather program (the default impl).
 """
 
 from __future__ import annotations
@@ -43,8 +50,8 @@ class Layer:
         return self._host
 
 
-def make_layer(shape: str, seed: int = 0, device: str = "cuda") -> Layer:
-    from kappa_amd.qwen3 import quantize_weight_per_channel
+def make_layer(shape: str, seed: int = 0, device: str = "cuda", per_tensor: bool = False) -> Layer:
+    from kappa_amd.qwen3 import quantize_weight, quantize_weight_per_channel
 
     s = SHAPES[shape]
     D, E, K, I = s["D"], s["E"], s["K"], s["I"]
@@ -54,9 +61,28 @@ def make_layer(shape: str, seed: int = 0, device: str = "cuda") -> Layer:
     ws = []
     for shp in ((E, D, I), (E, D, I), (E, I, D)):
         w = torch.randn(*shp, generator=g, device=device) * 0.02
-        ws.append(quantize_weight_per_channel(w))
+        ws.append(quantize_weight(w) if per_tensor else quantize_weight_per_channel(w))
         del w
     return Layer(D, E, K, I, router, *ws)
+
+
+def layer_cfg(layer: Layer, impl: str, **kw):
+    """A config that runs ``impl``'s array program at every token count: "ragged" is
+    ragged_jax with threshold 0; "gather_einsum" and "fixed_capacity" as named."""
+    from kappa_amd.qwen3 import moe_layer_config
+
+    if impl == "ragged":
+        kw = {"moe_impl": "ragged_jax", "moe_ragged_decode_token_threshold": 0, **kw}
+    else:
+        kw = {"moe_impl": impl, **kw}
+    return moe_layer_config(hidden=layer.D, experts=layer.E, top_k=layer.K, intermediate=layer.I, **kw)
+
+
+def forward_args(impl: str) -> dict:
+    """_moe_forward keywords that run ``impl``'s program at every token count."""
+    if impl == "ragged":
+        return {"impl": "ragged_jax", "decode_threshold": 0}
+    return {"impl": impl, "decode_threshold": 64}
 
 
 def make_x(T: int, D: int, seed: int = 0, device: str = "cuda", skew_router: torch.Tensor | None = None):
@@ -77,8 +103,9 @@ def skew_router(router: torch.Tensor, lam: float, seed: int = 6) -> torch.Tensor
     return r
 
 
-def oracle_rows(oracle, x_np, tokens, experts, host, act_bf16=True):
-    """Oracle h, y for the assignment rows (tokens[i], experts[i]); returns arrays in input order."""
+def oracle_rows(oracle, x_np, tokens, experts, host, act_bf16=True, *, impl):
+    """Oracle h, y of ``impl``'s program for the assignment rows (tokens[i], experts[i]),
+    in input order."""
     tokens = np.asarray(tokens, np.int32)
     experts = np.asarray(experts, np.int32)
     E = host["gate"][0].shape[0]
@@ -86,7 +113,7 @@ def oracle_rows(oracle, x_np, tokens, experts, host, act_bf16=True):
     st = tokens[order]
     counts = np.bincount(experts, minlength=E)
     off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
-    h, y = oracle.expert_ffn(x_np, off, st, host["gate"], host["up"], host["down"], act_bf16)
+    h, y = oracle.expert_ffn(x_np, off, st, host["gate"], host["up"], host["down"], act_bf16, impl=impl)
     inv = np.empty_like(order)
     inv[order] = np.arange(len(order))
     return h[inv], y[inv]

@@ -33,15 +33,20 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_status_strings():
     L = _lib.lib()
-    assert L.kmoe_abi_version() == 2
+    assert L.kmoe_abi_version() == 3 == _lib.ABI_VERSION
     assert b"gfx950" in L.kmoe_version()
     for s in range(6):
         assert L.kmoe_status_string(s)
     assert L.kmoe_status_string(99) == b"unknown status"
 
 
-def desc(T=4, D=128, E=8, K=2, I=64, act=_lib.DTYPE_BF16, thr=64, cap=0):
-    return _lib.KmoeDesc(T, D, E, K, I, act, thr, cap)
+def desc(T=4, D=128, E=8, K=2, I=64, act=_lib.DTYPE_BF16, thr=0, cap=0, impl=_lib.IMPL_RAGGED,
+         kernels=_lib.KERNELS_AUTO):  # fmt: skip
+    return _lib.KmoeDesc(T, D, E, K, I, act, impl, thr, cap, kernels)
+
+
+def packed(E=8, D=128, I=64, kind=_lib.SCALE_CHANNEL, s2=1):
+    return _lib.KmoePacked(1, 1, 1, s2, E, D, I, kind)
 
 
 def status_and_msg(st):
@@ -57,6 +62,10 @@ def status_and_msg(st):
         (dict(K=9), "top_k"),
         (dict(act=_lib.DTYPE_I8), "act_dtype"),
         (dict(cap=-1), "expert_capacity"),
+        (dict(impl=7), "unknown impl"),
+        (dict(impl=_lib.IMPL_FIXED_CAPACITY), "expert_capacity >= 1"),
+        (dict(impl=_lib.IMPL_GATHER_EINSUM, cap=4), "unless impl is fixed_capacity"),
+        (dict(kernels=5), "unknown kernels"),
     ],
 )
 def test_workspace_bytes_rejects_bad_desc(kw, frag):
@@ -72,6 +81,8 @@ def test_unsupported_sizes():
     assert L.kmoe_workspace_bytes(desc(D=8192), ctypes.byref(n)) == _lib.ERR_UNSUPPORTED
     sizes = _lib.KmoePackedSizes()
     assert L.kmoe_prepack_bytes(desc(D=96), sizes) == _lib.ERR_UNSUPPORTED
+    st = L.kmoe_workspace_bytes(desc(T=129, kernels=_lib.KERNELS_DECODE), ctypes.byref(n))
+    assert st == _lib.ERR_UNSUPPORTED and "at most 128 tokens" in L.kmoe_last_error().decode()
 
 
 def test_workspace_and_packed_sizes():
@@ -79,6 +90,13 @@ def test_workspace_and_packed_sizes():
     n = ctypes.c_size_t()
     assert L.kmoe_workspace_bytes(desc(T=4096, D=2048, E=128, K=8, I=768), ctypes.byref(n)) == _lib.OK
     M = 4096 * 8
+    # the ragged program above the threshold keeps h as two bf16 planes
+    assert n.value >= 2 * M * (2 * 768 + 2048) + 4 * 3 * M
+    ragged = n.value
+    assert L.kmoe_workspace_bytes(desc(T=4096, D=2048, E=128, K=8, I=768, thr=4096), ctypes.byref(n)) == _lib.OK
+    assert ragged - n.value >= 2 * M * 768 - 256  # at the threshold: the gather program, one plane
+    assert L.kmoe_workspace_bytes(desc(T=4096, D=2048, E=128, K=8, I=768, impl=_lib.IMPL_GATHER_EINSUM),
+                                  ctypes.byref(n)) == _lib.OK  # fmt: skip
     assert n.value >= 2 * M * (768 + 2048) + 4 * 3 * M
     sizes = _lib.KmoePackedSizes()
     assert L.kmoe_prepack_bytes(desc(D=2048, E=128, I=768), sizes) == _lib.OK
@@ -112,6 +130,37 @@ def test_forward_validation_before_any_hip_call():
         assert st == want and frag in msg, (over, st, msg)
 
 
+def test_gather_program_rejects_per_channel_scales():
+    """moe_take_dequant (kappa/qwen3/quant.py:71-74) cannot apply [E, 1, N] scales; the
+    ragged and fixed_capacity programs can. Checked before any HIP call."""
+    L = _lib.lib()
+    ch = weight(kind=_lib.SCALE_CHANNEL)
+    pt = weight(kind=_lib.SCALE_TENSOR)
+    f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
+
+    def fwd(d, g, p=None):
+        return status_and_msg(L.kmoe_forward(d, 1, f, g, g, g, p, 1, None, None, 1, 1 << 40, None))
+
+    st, msg = fwd(desc(impl=_lib.IMPL_GATHER_EINSUM), ch)
+    assert st == _lib.ERR_INVALID_ARG and "one scale per tensor" in msg
+    # ragged at or below the decode threshold runs the gather program (:219-223)
+    st, msg = fwd(desc(impl=_lib.IMPL_RAGGED, thr=64), ch)
+    assert st == _lib.ERR_INVALID_ARG and "one scale per tensor" in msg
+    st, msg = fwd(desc(impl=_lib.IMPL_GATHER_EINSUM, E=1, K=1), ch)  # [1, 1, N] broadcasts
+    assert st != _lib.ERR_INVALID_ARG, msg
+    for d in (desc(impl=_lib.IMPL_GATHER_EINSUM), desc(impl=_lib.IMPL_RAGGED, thr=0),
+              desc(impl=_lib.IMPL_FIXED_CAPACITY, cap=3)):  # fmt: skip
+        st, msg = fwd(d, pt)
+        assert st != _lib.ERR_INVALID_ARG, msg
+    st, msg = fwd(desc(impl=_lib.IMPL_RAGGED, thr=0), ch)
+    assert st != _lib.ERR_INVALID_ARG, msg
+    # packed experts carry the kind of their source scales
+    st, msg = fwd(desc(impl=_lib.IMPL_GATHER_EINSUM), ch, packed(kind=_lib.SCALE_CHANNEL))
+    assert st == _lib.ERR_INVALID_ARG and "one scale per tensor" in msg
+    st, msg = fwd(desc(impl=_lib.IMPL_GATHER_EINSUM), ch, packed(kind=_lib.SCALE_TENSOR))
+    assert st != _lib.ERR_INVALID_ARG, msg
+
+
 @pytest.mark.skipif(gpu_available(), reason="checks the no-device status")
 def test_valid_call_without_device_reports_no_device():
     L = _lib.lib()
@@ -127,14 +176,18 @@ def test_packed_argument_rules():
     L = _lib.lib()
     w = weight()
     f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
-    p = _lib.KmoePacked(1, 1, 1, None)
-    st = L.kmoe_forward(desc(), 1, f, w, w, w, p, 1, None, None, 1, 1 << 40, None)
+    st = L.kmoe_forward(desc(), 1, f, w, w, w, packed(s2=None), 1, None, None, 1, 1 << 40, None)
     assert st == _lib.ERR_INVALID_ARG
-    p = _lib.KmoePacked(1, 1, 1, 1)
-    st = L.kmoe_forward(desc(act=_lib.DTYPE_F32), 1, f, w, w, w, p, 1, None, None, 1, 1 << 40, None)
+    st = L.kmoe_forward(desc(act=_lib.DTYPE_F32), 1, f, w, w, w, packed(), 1, None, None, 1, 1 << 40, None)
     assert st == _lib.ERR_UNSUPPORTED
-    st = L.kmoe_forward(desc(D=96), 1, f, w, w, w, p, 1, None, None, 1, 1 << 40, None)
+    st = L.kmoe_forward(desc(D=96), 1, f, w, w, w, packed(D=96), 1, None, None, 1, 1 << 40, None)
     assert st == _lib.ERR_UNSUPPORTED
+    # the packed copy must hold the call's E, D and I (a mismatch would index past it)
+    for p in (packed(E=16), packed(D=256), packed(I=128)):
+        st = L.kmoe_forward(desc(), 1, f, w, w, w, p, 1, None, None, 1, 1 << 40, None)
+        assert st == _lib.ERR_INVALID_ARG and "packed experts hold" in L.kmoe_last_error().decode()
+    st = L.kmoe_forward(desc(), 1, f, w, w, w, packed(kind=_lib.SCALE_NONE), 1, None, None, 1, 1 << 40, None)
+    assert st == _lib.ERR_INVALID_ARG and "source_scale_kind" in L.kmoe_last_error().decode()
 
 
 def test_stage_entry_points_validate():
@@ -145,7 +198,8 @@ def test_stage_entry_points_validate():
     assert L.kmoe_combine(desc(), 1, None, 1, 1, None) == _lib.ERR_INVALID_ARG
     assert L.kmoe_expert_ffn(desc(), 1, 1, 1, 1, 1, None, None, None, None, 1, 1, None) == _lib.ERR_INVALID_ARG
     i8 = weight()
-    assert L.kmoe_prepack(desc(), f, i8, i8, _lib.KmoePacked(1, 1, 1, 1), None) == _lib.ERR_UNSUPPORTED
+    assert L.kmoe_prepack(desc(), f, i8, i8, packed(), None) == _lib.ERR_UNSUPPORTED
+    assert L.kmoe_prepack(desc(), i8, i8, i8, packed(E=4), None) == _lib.ERR_INVALID_ARG
     assert L.kmoe_to_compute_dtype(i8, 4, 0, 1, _lib.DTYPE_BF16, 1, None) == _lib.ERR_INVALID_ARG
     assert L.kmoe_quantize_per_channel(1, 4, 4, 1, _lib.DTYPE_I8, 1, 1, None) == _lib.ERR_INVALID_ARG
 
@@ -157,7 +211,7 @@ def test_zero_tokens_is_a_no_op_after_validation():
     w = weight()
     f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
     # T = 0 still validates, then reports the missing device (no launch is attempted)
-    st = L.kmoe_forward(desc(T=0), 1, f, w, w, w, None, 1, None, None, None, 0, None)
+    st = L.kmoe_forward(desc(T=0, thr=-1), 1, f, w, w, w, None, 1, None, None, None, 0, None)
     assert st == _lib.ERR_NO_DEVICE
 
 

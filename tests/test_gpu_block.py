@@ -16,7 +16,7 @@ import torch
 
 import oracle
 from inputs import BLOCK_SPECS, make_inputs, make_norm_scale
-from moe_cases import bf16_np, make_layer, make_x, mean_rel
+from moe_cases import bf16_np, forward_args, layer_cfg, make_layer, make_x, mean_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -77,10 +77,10 @@ def test_block_golden(dev, case):
     sc = torch.from_numpy(scale).to(dev).to(torch.bfloat16 if bf16 else torch.float32)
     out, idx, w = _moe_forward(
         h.reshape(1, spec.T, spec.D), r, g, u, d, num_experts=spec.E, num_experts_per_tok=spec.K,
-        decode_threshold=64, packed=None, return_routing=True, norm=(sc, eps),
+        packed=None, return_routing=True, norm=(sc, eps), **forward_args(spec.impl),
     )  # fmt: skip
     ref = oracle.forward_block(inp["x"], scale, inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K,
-                               act_bf16=bf16, eps=eps)  # fmt: skip
+                               act_bf16=bf16, impl=spec.impl, eps=eps)  # fmt: skip
     np.testing.assert_array_equal(idx.cpu().numpy(), ref["idx"])
     check_out(out.reshape(spec.T, spec.D).float().cpu().numpy(), ref["out"], bf16)
     gold = np.load(f"tests/golden/{spec.name}.npz")
@@ -103,9 +103,9 @@ def test_30b_fused_block_equals_separate_calls(dev, l30, T):
     """moe_block_ffn == h + moe_swiglu_ffn(rms_norm(h)), bit for bit; the norm is
     checked against the oracle on every row, the MoE half against the oracle
     by the block tests of test_gpu_parity."""
-    from kappa_amd.qwen3 import moe_block_ffn, moe_layer_config, moe_swiglu_ffn, rms_norm
+    from kappa_amd.qwen3 import moe_block_ffn, moe_swiglu_ffn, rms_norm
 
-    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
+    cfg = layer_cfg(l30, "ragged")
     h = make_x(T, l30.D, seed=900 + T).reshape(1, T, l30.D) * 4.0
     sc = _norm_scale(l30.D, T, dev)
     h2 = rms_norm(h, sc)
@@ -119,12 +119,9 @@ def test_30b_fused_block_equals_separate_calls(dev, l30, T):
 
 
 def test_30b_fused_block_fixed_capacity(dev, l30):
-    from kappa_amd.qwen3 import moe_block_ffn, moe_layer_config, moe_swiglu_ffn, rms_norm
+    from kappa_amd.qwen3 import moe_block_ffn, moe_swiglu_ffn, rms_norm
 
-    cfg = moe_layer_config(
-        hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_impl="fixed_capacity",
-        moe_capacity_factor=0.5,
-    )  # fmt: skip
+    cfg = layer_cfg(l30, "fixed_capacity", moe_capacity_factor=0.5)
     for T in (3, 64, 100, 1024):
         h = make_x(T, l30.D, seed=950 + T).reshape(1, T, l30.D)
         sc = _norm_scale(l30.D, 7 + T, dev)
@@ -134,9 +131,9 @@ def test_30b_fused_block_fixed_capacity(dev, l30):
 
 def test_zero_norm_scale_returns_the_residual(dev, l30):
     # rms_norm(h) * 0 = 0 and the block maps 0 to exactly 0: out == h
-    from kappa_amd.qwen3 import moe_block_ffn, moe_layer_config
+    from kappa_amd.qwen3 import moe_block_ffn
 
-    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
+    cfg = layer_cfg(l30, "ragged")
     for T in (3, 300):
         h = make_x(T, l30.D, seed=990 + T).reshape(1, T, l30.D)
         z = torch.zeros(l30.D, dtype=torch.bfloat16, device=dev)

@@ -1,9 +1,16 @@
 """HIP kernels against the oracle (GPU).
 
+Every layer call names the reference array program it is checked against
+(``impl``): the gather program (_moe_gather_einsum, kappa/qwen3/ffn_moe.py:74-104,
+the default impl and what ragged_* run at T <= the decode threshold), the ragged
+program (_moe_ragged, :174-216) or fixed_capacity (:107-158). The oracle restates
+each program's rounding points (oracle/moe_oracle.c) and is pinned by the golden
+vectors and property tests of the CPU suite.
+
 Bar: top-k indices and the dispatch arrays bit-exact; router logits bit-exact
-(the kernels and the oracle share the canonical summation order); layer
-outputs within max-abs 2e-2 and mean-rel 1e-3 in bf16, 1e-5 (relative to the
-output scale) in f32. mean-rel = mean|a - b| / mean|b|.
+(the kernels and the oracle share the canonical summation order); layer outputs
+within max-abs 2e-2 and mean-rel 1e-3 in bf16, 1e-5 (relative to the output scale)
+in f32. mean-rel = mean|a - b| / mean|b|.
 """
 
 from __future__ import annotations
@@ -13,8 +20,8 @@ import pytest
 import torch
 
 import oracle
-from inputs import GOLDEN_SPECS, Spec, make_inputs
-from moe_cases import bf16_np, make_layer, make_x, mean_rel, oracle_rows, skew_router
+from inputs import CAPACITY_SPECS, GOLDEN_SPECS, Spec, make_inputs
+from moe_cases import bf16_np, forward_args, layer_cfg, make_layer, make_x, mean_rel, oracle_rows, skew_router
 
 pytestmark = pytest.mark.gpu
 
@@ -59,6 +66,7 @@ def spec_to_dev(spec: Spec, inp: dict, dev):
 def check_out(out: np.ndarray, ref: np.ndarray, bf16: bool, what: str = "out"):
     if bf16:
         d = np.abs(out - ref)
+        print(f"{what}: max-abs {d.max():.2e} mean-rel {mean_rel(out, ref):.2e}")
         assert d.max() <= BF16_MAX_ABS, f"{what}: max-abs {d.max():.3e}"
         assert mean_rel(out, ref) <= BF16_MEAN_REL, f"{what}: mean-rel {mean_rel(out, ref):.3e}"
     else:
@@ -67,7 +75,7 @@ def check_out(out: np.ndarray, ref: np.ndarray, bf16: bool, what: str = "out"):
 
 
 def check_inter(out: np.ndarray, ref: np.ndarray, what: str):
-    """bf16 intermediates (h, y).
+    """bf16 intermediates (h of the gather program, y).
 
     The MFMA kernels and the oracle add the same products in different fp32 orders, so
     g, u and y may round to a neighbouring bf16 number; silu amplifies a flip in g (up to
@@ -79,37 +87,60 @@ def check_inter(out: np.ndarray, ref: np.ndarray, what: str):
     top = float(np.abs(ref).max())
     diff_frac = float(np.mean(d > 0))
     print(f"{what}: mean-rel {mean_rel(out, ref):.2e} max-abs {d.max():.2e} (max|ref| {top:.2e}) "
-          f"not-identical {diff_frac:.4f}")
+          f"not-identical {diff_frac:.4f}")  # fmt: skip
     assert mean_rel(out, ref) <= BF16_MEAN_REL, f"{what}: mean-rel {mean_rel(out, ref):.3e}"
     assert d.max() <= 2.0**-6 * top, f"{what}: max-abs {d.max():.3e} vs max|ref| {top:.3e}"
     assert diff_frac <= 0.10, f"{what}: {diff_frac:.3f} of elements differ"
 
 
+def check_h32(h_dev: torch.Tensor, ref: np.ndarray, I: int, what: str = "h"):
+    """The ragged program's f32 h: the kernels keep it as bf16 hi + lo (~2^-17 relative)
+    and sum in another f32 order than the oracle; a bf16-rounded h would miss by 2^-9."""
+    from kappa_amd.qwen3.moe_stages import h_float
 
-# --- golden cases: the whole block through moe_swiglu_ffn ----------------------
+    h = h_float(h_dev, I).cpu().numpy()
+    d = np.abs(h - ref)
+    top = float(np.abs(ref).max())
+    print(f"{what}: max-abs {d.max():.2e} (max|ref| {top:.2e}) mean-rel {mean_rel(h, ref):.2e}")
+    assert d.max() <= 3e-5 * top, f"{what}: {d.max():.3e} vs max|ref| {top:.3e}"
+    assert mean_rel(h, ref) <= 2e-5
 
 
-@pytest.mark.parametrize("spec", GOLDEN_SPECS, ids=[s.name for s in GOLDEN_SPECS])
-def test_golden_block(dev, spec):
-    from kappa_amd.qwen3 import moe_layer_config
+# --- golden cases: the whole block through the C ABI --------------------------
+
+
+def _spec_forward(spec, inp, dev, kernels):
     from kappa_amd.qwen3.ffn_moe import _moe_forward
+
+    x, r, (g, u, d) = spec_to_dev(spec, inp, dev)
+    return _moe_forward(
+        x.reshape(1, spec.T, spec.D), r, g, u, d, num_experts=spec.E, num_experts_per_tok=spec.K,
+        packed=None, return_routing=True, kernels=kernels, **forward_args(spec.impl),
+    )  # fmt: skip
+
+
+@pytest.mark.parametrize("kernels", ["auto", "grouped"])
+@pytest.mark.parametrize("spec", GOLDEN_SPECS, ids=[s.name for s in GOLDEN_SPECS])
+def test_golden_block(dev, spec, kernels):
+    """Each golden case through the program it restates, on the token-count kernel
+    family and on the grouped GEMMs."""
+    from kappa_amd import _lib
 
     inp = make_inputs(spec)
     bf16 = spec.act == "bf16"
-    x, r, (g, u, d) = spec_to_dev(spec, inp, dev)
-    out, idx, w = _moe_forward(
-        x.reshape(1, spec.T, spec.D), r, g, u, d, num_experts=spec.E, num_experts_per_tok=spec.K,
-        decode_threshold=64, packed=None, return_routing=True,
-    )  # fmt: skip
-    ref = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=bf16)
+    fam = _lib.KERNELS_AUTO if kernels == "auto" else _lib.KERNELS_GROUPED
+    out, idx, w = _spec_forward(spec, inp, dev, fam)
+    ref = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=bf16,
+                         impl=spec.impl)  # fmt: skip
     np.testing.assert_array_equal(idx.cpu().numpy(), ref["idx"])
     wg = w.float().cpu().numpy()
     assert np.all(np.abs(wg - ref["w"]) <= (2.0**-8 if bf16 else 2.0**-22) * np.abs(ref["w"]))
-    check_out(out.reshape(spec.T, spec.D).float().cpu().numpy(), ref["out"], bf16)
-    # and against the golden vectors written from the reference restatement
+    got = out.reshape(spec.T, spec.D).float().cpu().numpy()
+    check_out(got, ref["out"], bf16)
+    # and against the golden vectors written from the literal restatement
     gold = np.load(f"tests/golden/{spec.name}.npz")
     np.testing.assert_array_equal(idx.cpu().numpy(), gold["idx"])
-    check_out(out.reshape(spec.T, spec.D).float().cpu().numpy(), gold["out"], bf16, "vs golden")
+    check_out(got, gold["out"], bf16, "vs golden")
 
 
 # --- the 30B-A3B and 235B-A22B layers ----------------------------------------
@@ -117,7 +148,14 @@ def test_golden_block(dev, spec):
 
 @pytest.fixture(scope="module")
 def l30(dev):
+    """Per-output-channel scales (the benchmark layer)."""
     return make_layer("30b", seed=0)
+
+
+@pytest.fixture(scope="module")
+def l30t(dev):
+    """Per-tensor bf16 scales (the reference's quantize_weight): runs every program."""
+    return make_layer("30b", seed=5, per_tensor=True)
 
 
 def _route_and_dispatch(x, layer_router, E, K):
@@ -148,51 +186,90 @@ def _check_routing(x, router, E, K, r, d):
     return xn, idx, w, od
 
 
-@pytest.mark.parametrize("T", [1, 8, 32, 64])
-def test_30b_decode_full(dev, l30, T):
-    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+def _decode_full(layer, T, impl, seed):
+    """Whole decode call and its stages against the oracle of ``impl``'s program."""
+    from kappa_amd.qwen3 import moe_stages, moe_swiglu_ffn
 
-    x = make_x(T, l30.D, seed=T)
-    r, d = _route_and_dispatch(x, l30.router, l30.E, l30.K)
-    xn, idx, w, od = _check_routing(x, l30.router, l30.E, l30.K, r, d)
-    host = l30.host()
-    h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K)
-    ho, yo = oracle.expert_ffn(xn, od["offsets"], od["sorted_token"], host["gate"], host["up"], host["down"], True)
-    check_inter(bf16_np(h), ho, "h")
+    x = make_x(T, layer.D, seed=seed)
+    r, d = _route_and_dispatch(x, layer.router, layer.E, layer.K)
+    xn, idx, w, od = _check_routing(x, layer.router, layer.E, layer.K, r, d)
+    host = layer.host()
+    h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl=impl)
+    ho, yo = oracle.expert_ffn(xn, od["offsets"], od["sorted_token"], host["gate"], host["up"], host["down"], True,
+                               impl=impl)  # fmt: skip
+    if impl == "ragged":
+        check_h32(h, ho, layer.I)
+    else:
+        check_inter(bf16_np(h), ho, "h")
     check_inter(bf16_np(y), yo, "y")
-    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
-    out = moe_swiglu_ffn(x.reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
-    ref = oracle.combine(yo, od["inv"], w, True)
-    check_out(bf16_np(out.reshape(T, l30.D)), ref, True)
+    out = moe_swiglu_ffn(x.reshape(1, T, layer.D), layer.router, layer.gate, layer.up, layer.down,
+                         cfg=layer_cfg(layer, impl))  # fmt: skip
+    ref = oracle.combine(yo, od["inv"], w, True, impl=impl)
+    check_out(bf16_np(out.reshape(T, layer.D)), ref, True)
+    # the staged combine follows the same program
+    staged = moe_stages.combine(y, d["inv"], r["w"], k=layer.K, impl=impl)
+    check_out(bf16_np(staged), ref, True, "staged combine")
 
 
-@pytest.mark.parametrize("T", [512, 2048, 4096])
-def test_30b_prefill_sampled(dev, l30, T):
-    _prefill_sampled(l30, T, seed=100 + T)
+@pytest.mark.parametrize("T", [1, 8, 32, 64])
+def test_30b_decode_ragged_per_channel(dev, l30, T):
+    """The benchmark decode configuration: per-channel W8 on the ragged program
+    (ragged_jax, decode threshold 0)."""
+    _decode_full(l30, T, "ragged", seed=T)
 
 
-def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48):
-    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+@pytest.mark.parametrize("T", [1, 8, 32, 64])
+def test_30b_decode_gather_per_tensor(dev, l30t, T):
+    """The reference's default decode program (gather_einsum) on per-tensor W8."""
+    _decode_full(l30t, T, "gather_einsum", seed=40 + T)
+
+
+@pytest.mark.parametrize("T", [8, 64])
+def test_30b_decode_ragged_per_tensor(dev, l30t, T):
+    _decode_full(l30t, T, "ragged", seed=80 + T)
+
+
+def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48, impl="ragged", cfg=None):
+    from kappa_amd.qwen3 import moe_stages, moe_swiglu_ffn
 
     router = layer.router if router is None else router
     x = make_x(T, layer.D, seed=seed) if x is None else x
     r, d = _route_and_dispatch(x, router, layer.E, layer.K)
     xn, idx, w, od = _check_routing(x, router, layer.E, layer.K, r, d)
-    h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K)
-    cfg = moe_layer_config(hidden=layer.D, experts=layer.E, top_k=layer.K, intermediate=layer.I)
-    out = moe_swiglu_ffn(x.reshape(1, T, layer.D), router, layer.gate, layer.up, layer.down, cfg=cfg)
+    h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl=impl)
+    out = moe_swiglu_ffn(x.reshape(1, T, layer.D), router, layer.gate, layer.up, layer.down,
+                         cfg=cfg or layer_cfg(layer, impl))  # fmt: skip
     rng = np.random.default_rng(seed)
     toks = np.sort(rng.choice(T, size=min(n_tok, T), replace=False))
     toks = np.unique(np.concatenate([toks, [0, T - 1]]))
     rows_t = np.repeat(toks, layer.K)
     rows_e = idx[toks].reshape(-1)
-    ho, yo = oracle_rows(oracle, xn, rows_t, rows_e, layer.host())
+    ho, yo = oracle_rows(oracle, xn, rows_t, rows_e, layer.host(), impl=impl)
     pos = od["inv"].reshape(T, layer.K)[toks].reshape(-1)
-    check_inter(bf16_np(h)[pos], ho, "h rows")
+    if impl == "ragged":
+        check_h32(h[torch.from_numpy(pos).to(h.device).long()], ho, layer.I, "h rows")
+    else:
+        check_inter(bf16_np(h)[pos], ho, "h rows")
     check_inter(bf16_np(y)[pos], yo, "y rows")
-    ref = oracle.combine(yo, np.arange(len(rows_t), dtype=np.int32), w[toks], True)
+    ref = oracle.combine(yo, np.arange(len(rows_t), dtype=np.int32), w[toks], True, impl=impl)
     check_out(bf16_np(out.reshape(T, layer.D))[toks], ref, True, "out rows")
     return od
+
+
+@pytest.mark.parametrize("T", [512, 2048, 4096])
+def test_30b_prefill_ragged(dev, l30, T):
+    """The prefill chunks under the reference's ragged program (ragged_jax with its
+    default threshold of 64: these sizes run _moe_ragged)."""
+    from kappa_amd.qwen3 import moe_layer_config
+
+    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_impl="ragged_jax")
+    _prefill_sampled(l30, T, seed=100 + T, cfg=cfg)
+
+
+@pytest.mark.parametrize("T", [512, 4096])
+def test_30b_prefill_gather_per_tensor(dev, l30t, T):
+    """The gather program (the default impl) at prefill sizes on the grouped GEMMs."""
+    _prefill_sampled(l30t, T, seed=150 + T, impl="gather_einsum", n_tok=24)
 
 
 @pytest.mark.parametrize("T", [65, 100, 128])
@@ -220,29 +297,27 @@ def test_30b_skewed_routing(dev, l30):
 
 
 def test_235b_layer(dev):
-    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+    from kappa_amd.qwen3 import moe_block_ffn, moe_stages, moe_swiglu_ffn, rms_norm
 
     layer = make_layer("235b", seed=1)
+    cfg = layer_cfg(layer, "ragged")
     _prefill_sampled(layer, 16, seed=16, n_tok=16)
     _prefill_sampled(layer, 100, seed=100, n_tok=16)  # the row-group kernels
     _prefill_sampled(layer, 2048, seed=2048, n_tok=24)
-    # T = 1 and 2: the whole layer (fused down + combine at T = 1, each wave
-    # holding 12 of the 24 chunks of the reduction) against the staged calls
-    cfg = moe_layer_config(hidden=layer.D, experts=layer.E, top_k=layer.K, intermediate=layer.I)
     # the block call at T = 100: the split router normalising 4096-wide rows
     # (four tokens per block)
-    from kappa_amd.qwen3 import moe_block_ffn, rms_norm
-
     h = make_x(100, layer.D, seed=101).reshape(1, 100, layer.D)
     sc = (1.0 + 0.1 * torch.randn(layer.D, device=dev)).to(torch.bfloat16)
     composed = h + moe_swiglu_ffn(rms_norm(h, sc), layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
     assert torch.equal(moe_block_ffn(h, sc, layer.router, layer.gate, layer.up, layer.down, cfg=cfg), composed)
+    # T = 1 and 2: the whole layer (fused down + combine, each wave holding 12 of
+    # the 24 chunks of the reduction) against the staged calls
     for T in (1, 2):
         _prefill_sampled(layer, T, seed=T, n_tok=T)
         x = make_x(T, layer.D, seed=T)
         r, d = _route_and_dispatch(x, layer.router, layer.E, layer.K)
-        h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K)
-        staged = moe_stages.combine(y, d["inv"], r["w"], k=layer.K)
+        h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl="ragged")
+        staged = moe_stages.combine(y, d["inv"], r["w"], k=layer.K, impl="ragged")
         out = moe_swiglu_ffn(x.reshape(1, T, layer.D), layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
         assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
     del layer
@@ -252,22 +327,28 @@ def test_235b_layer(dev):
 # --- cross-checks between kernel families, determinism, edge cases -----------
 
 
-def test_decode_and_prefill_kernels_agree_at_threshold(dev, l30):
-    from kappa_amd.qwen3 import moe_layer_config, moe_swiglu_ffn
+@pytest.mark.parametrize("impl", ["ragged", "gather_einsum"])
+def test_decode_and_grouped_kernels_agree(dev, l30, l30t, impl):
+    """The GEMV-style kernels and the grouped GEMMs follow the same program: they agree
+    within the bar (scripts/verify_qwen3_moe_impls.py:61-70 cross-checks the
+    reference's own paths the same way)."""
+    from kappa_amd import _lib
+    from kappa_amd.qwen3.ffn_moe import _moe_forward
 
-    for T in (64, 65):
-        x = make_x(T, l30.D, seed=300 + T).reshape(1, T, l30.D)
-        outs = []
-        for thr in (64, 0):
-            cfg = moe_layer_config(
-                hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_ragged_decode_token_threshold=thr
-            )
-            outs.append(bf16_np(moe_swiglu_ffn(x, l30.router, l30.gate, l30.up, l30.down, cfg=cfg)))
+    layer = l30 if impl == "ragged" else l30t
+    for T in (1, 16, 64, 65, 128):
+        x = make_x(T, layer.D, seed=300 + T).reshape(1, T, layer.D)
+        outs = [
+            bf16_np(_moe_forward(x, layer.router, layer.gate, layer.up, layer.down, num_experts=layer.E,
+                                 num_experts_per_tok=layer.K, packed=None, kernels=k, **forward_args(impl)))
+            for k in (_lib.KERNELS_AUTO, _lib.KERNELS_GROUPED)
+        ]  # fmt: skip
         check_out(outs[0], outs[1], True, f"T={T}")
 
 
+@pytest.mark.parametrize("impl", ["ragged", "gather_einsum"])
 @pytest.mark.parametrize("T", [1, 2, 8, 16, 17, 40, 64, 65, 100, 128])
-def test_whole_block_matches_staged_path(dev, l30, T):
+def test_whole_block_matches_staged_path(dev, l30, l30t, T, impl):
     """At T <= 128 the whole-block call routes with the split router (many
     blocks per token); the staged calls use the one-block-per-token router.
     Both follow the canonical summation order, so selections, weights and
@@ -277,21 +358,22 @@ def test_whole_block_matches_staged_path(dev, l30, T):
     from kappa_amd.qwen3 import moe_stages
     from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _moe_forward
 
-    for router in (l30.router, skew_router(l30.router, lam=1.5)):
-        x = make_x(T, l30.D, seed=700 + T)
+    layer = l30 if impl == "ragged" else l30t
+    for router in (layer.router, skew_router(layer.router, lam=1.5)):
+        x = make_x(T, layer.D, seed=700 + T)
         x[:, 0] = 1.0
-        r, d = _route_and_dispatch(x, router, l30.E, l30.K)
-        h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K)
-        staged = moe_stages.combine(y, d["inv"], r["w"], k=l30.K)
-        packed = PACK_CACHE.get(l30.gate, l30.up, l30.down)
+        r, d = _route_and_dispatch(x, router, layer.E, layer.K)
+        h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl=impl)
+        staged = moe_stages.combine(y, d["inv"], r["w"], k=layer.K, impl=impl)
+        packed = PACK_CACHE.get(layer.gate, layer.up, layer.down)
         for _ in range(2):
             out, idx, w = _moe_forward(
-                x.reshape(1, T, l30.D), router, l30.gate, l30.up, l30.down, num_experts=l30.E,
-                num_experts_per_tok=l30.K, decode_threshold=64, packed=packed, return_routing=True,
+                x.reshape(1, T, layer.D), router, layer.gate, layer.up, layer.down, num_experts=layer.E,
+                num_experts_per_tok=layer.K, packed=packed, return_routing=True, **forward_args(impl),
             )  # fmt: skip
             assert torch.equal(idx, r["idx"])
             assert torch.equal(w.float(), r["w"])
-            assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
+            assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
 
 
 @pytest.mark.parametrize("T,K", [(1, 8), (2, 4), (2, 8), (3, 8), (8, 8)])
@@ -311,34 +393,36 @@ def test_whole_block_with_drops_matches_staged_path(dev, l30, T, K):
     d = moe_stages.dispatch(r["idx"], r["hist"], num_experts=l30.E, capacity=1)
     if T > 1:
         assert bool((d["inv"] < 0).any())
-    h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=K, capacity=1)
-    staged = moe_stages.combine(y, d["inv"], r["w"], k=K)
+    h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=K, impl="fixed_capacity", capacity=1)
+    staged = moe_stages.combine(y, d["inv"], r["w"], k=K, impl="fixed_capacity")
     out = _moe_forward(
         x.reshape(1, T, l30.D), router, l30.gate, l30.up, l30.down, num_experts=l30.E, num_experts_per_tok=K,
-        decode_threshold=64, packed=PACK_CACHE.get(l30.gate, l30.up, l30.down), capacity=1,
+        impl="fixed_capacity", decode_threshold=64, packed=PACK_CACHE.get(l30.gate, l30.up, l30.down), capacity=1,
     )  # fmt: skip
     assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
 
 
+@pytest.mark.parametrize("impl", ["ragged", "gather_einsum"])
 @pytest.mark.parametrize("T,K", [(1, 1), (1, 8), (3, 2), (4, 2), (8, 1), (2, 3), (2, 8), (3, 8), (4, 8), (13, 2), (5, 6)])
-def test_fused_down_combine_shapes(dev, l30, T, K):
+def test_fused_down_combine_shapes(dev, l30, l30t, T, K, impl):
     """The whole-block call at T * K <= 32 (down projection and combine in one
     kernel; blocks of 8 / K tokens, two waves per assignment, 16 combine
     threads per token; a last block with fewer tokens) against the staged
-    calls, bit for bit."""
+    calls, bit for bit, on both rounding chains."""
     from kappa_amd.qwen3 import moe_stages
     from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _moe_forward
 
-    x = make_x(T, l30.D, seed=830 + 10 * T + K)
-    r = moe_stages.route(x, l30.router, num_experts=l30.E, k=K)
-    d = moe_stages.dispatch(r["idx"], r["hist"], num_experts=l30.E)
-    h, y = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=K)
-    staged = moe_stages.combine(y, d["inv"], r["w"], k=K)
+    layer = l30 if impl == "ragged" else l30t
+    x = make_x(T, layer.D, seed=830 + 10 * T + K)
+    r = moe_stages.route(x, layer.router, num_experts=layer.E, k=K)
+    d = moe_stages.dispatch(r["idx"], r["hist"], num_experts=layer.E)
+    h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=K, impl=impl)
+    staged = moe_stages.combine(y, d["inv"], r["w"], k=K, impl=impl)
     out = _moe_forward(
-        x.reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, num_experts=l30.E, num_experts_per_tok=K,
-        decode_threshold=64, packed=PACK_CACHE.get(l30.gate, l30.up, l30.down),
+        x.reshape(1, T, layer.D), layer.router, layer.gate, layer.up, layer.down, num_experts=layer.E,
+        num_experts_per_tok=K, packed=PACK_CACHE.get(layer.gate, layer.up, layer.down), **forward_args(impl),
     )  # fmt: skip
-    assert torch.equal(out.reshape(T, l30.D), staged.reshape(T, l30.D))
+    assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
 
 
 @pytest.mark.parametrize("T", [1, 4, 8, 15, 63])
@@ -351,31 +435,39 @@ def test_decode_batch_invariance(dev, l30, T):
     to T = 4 and T = 16). Between T = 16 and 17 the
     gate/up reduction goes from eight wave chains to four, a different
     grouping of the same sum, so that pair is not bit-identical."""
-    from kappa_amd.qwen3 import moe_layer_config, moe_swiglu_ffn
+    from kappa_amd.qwen3 import moe_swiglu_ffn
 
-    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
+    cfg = layer_cfg(l30, "ragged")
     x = make_x(T + 1, l30.D, seed=880 + T)
     a = moe_swiglu_ffn(x[:T].reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
     b = moe_swiglu_ffn(x.reshape(1, T + 1, l30.D), l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
     assert torch.equal(a.reshape(T, l30.D), b.reshape(T + 1, l30.D)[:T])
 
 
-def test_layout_native_experts_match_packed(dev, l30):
+@pytest.mark.parametrize("impl", ["ragged", "gather_einsum"])
+def test_layout_native_experts_match_packed(dev, l30, l30t, impl):
     from kappa_amd.qwen3 import moe_stages
 
+    layer = l30 if impl == "ragged" else l30t
     for T in (8, 200):
-        x = make_x(T, l30.D, seed=400 + T)
-        r, d = _route_and_dispatch(x, l30.router, l30.E, l30.K)
-        h1, y1 = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K)
-        h2, y2 = moe_stages.expert_ffn(x, d, l30.gate, l30.up, l30.down, k=l30.K, layout_native=True)
-        check_inter(bf16_np(h1), bf16_np(h2), "h")
+        x = make_x(T, layer.D, seed=400 + T)
+        r, d = _route_and_dispatch(x, layer.router, layer.E, layer.K)
+        h1, y1 = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl=impl)
+        h2, y2 = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl=impl,
+                                       layout_native=True)  # fmt: skip
+        if impl == "ragged":
+            from kappa_amd.qwen3.moe_stages import h_float
+
+            check_h32(h1, h_float(h2, layer.I).cpu().numpy(), layer.I)
+        else:
+            check_inter(bf16_np(h1), bf16_np(h2), "h")
         check_inter(bf16_np(y1), bf16_np(y2), "y")
 
 
 def test_repeat_runs_are_bitwise_identical(dev, l30):
-    from kappa_amd.qwen3 import moe_layer_config, moe_swiglu_ffn
+    from kappa_amd.qwen3 import moe_swiglu_ffn
 
-    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I)
+    cfg = layer_cfg(l30, "ragged")
     for T in (7, 333):
         x = make_x(T, l30.D, seed=500 + T).reshape(1, T, l30.D)
         a = moe_swiglu_ffn(x, l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
@@ -391,22 +483,27 @@ def test_ragged_token_counts(dev, T):
     inp = make_inputs(spec)
     x, r, (g, u, d) = spec_to_dev(spec, inp, dev)
     x = x[:T].reshape(1, T, spec.D)
-    cfg = moe_layer_config(hidden=128, experts=16, top_k=4, intermediate=64)
+    # threshold -1: the ragged program also at T = 0 (T <= 0 would select the gather
+    # program, which has no per-channel form)
+    cfg = moe_layer_config(hidden=128, experts=16, top_k=4, intermediate=64, moe_impl="ragged_jax",
+                           moe_ragged_decode_token_threshold=-1)  # fmt: skip
     out = moe_swiglu_ffn(x, r, g, u, d, cfg=cfg)
     assert out.shape == (1, T, 128) and out.dtype == torch.bfloat16
     if T:
-        ref = oracle.forward(inp["x"][:T], inp["router"], inp["gate"], inp["up"], inp["down"], k=4, act_bf16=True)
+        ref = oracle.forward(inp["x"][:T], inp["router"], inp["gate"], inp["up"], inp["down"], k=4, act_bf16=True,
+                             impl="ragged")  # fmt: skip
         check_out(bf16_np(out.reshape(T, 128)), ref["out"], True)
 
 
 @pytest.mark.parametrize(
     "spec",
     [
-        Spec("odd_e_bf16", T=5, D=100, E=9, K=3, I=32, base_seed=150),  # E % 2 != 0: per-element router loads
+        Spec("odd_e_bf16", T=5, D=100, E=9, K=3, I=32, base_seed=150, impl="ragged"),  # per-element router loads
         Spec("tiny_e_f32", T=3, D=64, E=3, K=1, I=32, act="f32", weights="f32", router="f32", base_seed=151),
-        Spec("e33_qrouter", T=17, D=192, E=33, K=4, I=64, router="w8t", scale_dtype="bf16", base_seed=152),
-        Spec("wide_d_bf16", T=9, D=4096, E=64, K=6, I=64, base_seed=153),  # 64 slices: Q = 16 groups
-        Spec("e200_bf16", T=40, D=256, E=200, K=8, I=32, base_seed=154),  # four experts per lane in the finish
+        Spec("e33_qrouter", T=17, D=192, E=33, K=4, I=64, router="w8t", scale_dtype="bf16", base_seed=152,
+             impl="ragged"),  # fmt: skip
+        Spec("wide_d_bf16", T=9, D=4096, E=64, K=6, I=64, base_seed=153, impl="ragged"),  # 64 slices: Q = 16 groups
+        Spec("e200_bf16", T=40, D=256, E=200, K=8, I=32, weights="w8t", scale_dtype="bf16", base_seed=154),
     ],
     ids=lambda s: s.name,
 )
@@ -414,19 +511,43 @@ def test_split_router_shapes_match_oracle(dev, spec):
     """The whole-block call at T <= 64 routes with the split router: top-k
     indices bit-exact against the oracle (its canonical order) and the output
     within tolerance, on shapes that take its less common paths."""
-    from kappa_amd.qwen3.ffn_moe import _moe_forward
+    from kappa_amd import _lib
 
     inp = make_inputs(spec)
     bf16 = spec.act == "bf16"
-    x, r, (g, u, d) = spec_to_dev(spec, inp, dev)
-    out, idx, w = _moe_forward(
-        x.reshape(1, spec.T, spec.D), r, g, u, d, num_experts=spec.E, num_experts_per_tok=spec.K,
-        decode_threshold=64, packed=None, return_routing=True,
-    )  # fmt: skip
-    ref = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=bf16)
+    out, idx, w = _spec_forward(spec, inp, dev, _lib.KERNELS_AUTO)
+    ref = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K, act_bf16=bf16,
+                         impl=spec.impl)  # fmt: skip
     np.testing.assert_array_equal(idx.cpu().numpy(), ref["idx"])
     np.testing.assert_array_equal(w.float().cpu().numpy(), ref["w"])
     check_out(out.reshape(spec.T, spec.D).float().cpu().numpy(), ref["out"], bf16)
+
+
+def test_legacy_entry_point_runs_the_gather_program(dev, l30t):
+    """moe_swiglu_ffn_legacy (kappa/qwen3/ffn_moe.py:302-316) ignores config flags and
+    always runs the gather program: one decode and one prefill token count."""
+    from kappa_amd.qwen3 import moe_swiglu_ffn_legacy
+
+    host = l30t.host()
+    for T, n_tok in ((8, 8), (512, 16)):
+        x = make_x(T, l30t.D, seed=1200 + T)
+        out = moe_swiglu_ffn_legacy(x.reshape(1, T, l30t.D), l30t.router, l30t.gate, l30t.up, l30t.down,
+                                    num_experts=l30t.E, num_experts_per_tok=l30t.K)  # fmt: skip
+        xn = bf16_np(x)
+        idx, w = oracle.topk_softmax(oracle.router_logits(xn, l30t.router.float().cpu().numpy()), l30t.K, True)
+        toks = np.unique(np.concatenate([np.random.default_rng(T).choice(T, n_tok, replace=False), [0, T - 1]]))
+        rows_t = np.repeat(toks, l30t.K)
+        _, yo = oracle_rows(oracle, xn, rows_t, idx[toks].reshape(-1), host, impl="gather_einsum")
+        ref = oracle.combine(yo, np.arange(len(rows_t), dtype=np.int32), w[toks], True, impl="gather_einsum")
+        check_out(bf16_np(out.reshape(T, l30t.D))[toks], ref, True, f"legacy T={T}")
+
+
+def test_gather_program_rejects_per_channel_layer(dev, l30):
+    from kappa_amd.qwen3 import moe_swiglu_ffn
+
+    x = make_x(4, l30.D, seed=1).reshape(1, 4, l30.D)
+    with pytest.raises(ValueError, match="one scale per tensor"):
+        moe_swiglu_ffn(x, l30.router, l30.gate, l30.up, l30.down, cfg=layer_cfg(l30, "gather_einsum"))
 
 
 # --- weights ------------------------------------------------------------------
@@ -446,6 +567,17 @@ def test_quantiser_matches_oracle(dev):
     qo2, so2 = oracle.quantize_per_channel(wb.float().cpu().numpy())
     np.testing.assert_array_equal(q2.cpu().numpy(), qo2)
     np.testing.assert_array_equal(s2.cpu().numpy(), so2)
+
+
+def test_per_tensor_quantiser_matches_oracle(dev):
+    from kappa_amd.qwen3 import quantize_weight
+
+    rng = np.random.default_rng(15)
+    w = (rng.standard_normal((4, 256, 48)) * 0.02).astype(np.float32)
+    q, s = quantize_weight(torch.from_numpy(w).to(dev), scale_dtype=torch.float32)
+    qo, so = oracle.quantize_per_tensor(w)
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    assert float(s) == float(so)
 
 
 def test_to_compute_dtype_matches_reference_rule(dev):
@@ -468,6 +600,7 @@ def test_to_compute_dtype_matches_reference_rule(dev):
 
 
 def test_prepack_layout(dev):
+    from kappa_amd import _lib
     from kappa_amd.qwen3 import Q8Weight, prepack_moe_experts
 
     rng = np.random.default_rng(14)
@@ -476,6 +609,7 @@ def test_prepack_layout(dev):
     ss = [(rng.random((E, 1, n)) * 0.01).astype(np.float32) for n in (I, I, D)]
     ws = [Q8Weight(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)) for q, s in zip(qs, ss)]
     p = prepack_moe_experts(*ws)
+    assert (p.num_experts, p.hidden, p.intermediate, p.source_scale_kind) == (E, D, I, _lib.SCALE_CHANNEL)
     w13 = p.w13.cpu().numpy().reshape(E, I // 16, 2, D // 16, 16, 16)
     # cell [e, ig, which, kg, col, kk] = src[e, kg*16+kk, ig*16+col]
     for which in (0, 1):
@@ -484,25 +618,30 @@ def test_prepack_layout(dev):
     w2 = p.w2.cpu().numpy().reshape(E, D // 16, I // 16, 16, 16)
     src = qs[2].reshape(E, I // 16, 16, D // 16, 16)  # e, kg, kk, dg, col
     np.testing.assert_array_equal(w2, src.transpose(0, 3, 1, 4, 2))
+    # the scales as given (f32): the kernels round them to bf16 only for the
+    # gather and fixed_capacity programs
     s13 = p.s13.cpu().numpy().reshape(E, I // 16, 2, 16)
     for which in (0, 1):
-        np.testing.assert_array_equal(s13[:, :, which], oracle.bf16_round(ss[which]).reshape(E, I // 16, 16))
-    np.testing.assert_array_equal(p.s2.cpu().numpy().reshape(E, D), oracle.bf16_round(ss[2]).reshape(E, D))
+        np.testing.assert_array_equal(s13[:, :, which], ss[which].reshape(E, I // 16, 16))
+    np.testing.assert_array_equal(p.s2.cpu().numpy().reshape(E, D), ss[2].reshape(E, D))
+    pt = prepack_moe_experts(*[Q8Weight(w.values, torch.tensor(0.01, device=dev)) for w in ws])
+    assert pt.source_scale_kind == _lib.SCALE_TENSOR
 
 
 # --- fixed_capacity (token dropping, kappa/qwen3/ffn_moe.py:107-158) ----------
 
-from inputs import CAPACITY_SPECS  # noqa: E402
 
-
+@pytest.mark.parametrize("kernels", ["auto", "grouped"])
 @pytest.mark.parametrize("case", CAPACITY_SPECS, ids=[c[0].name for c in CAPACITY_SPECS])
-def test_fixed_capacity_golden(dev, case):
+def test_fixed_capacity_golden(dev, case, kernels):
     """moe_swiglu_ffn with moe_impl='fixed_capacity' against the oracle and the
-    golden restatement: the same slot limit, the same dropped assignments."""
+    golden restatement: the same slot limit, the same dropped assignments, the
+    bf16 expert chain and the bf16 scatter-add combine."""
     import dataclasses
 
-    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
-    from kappa_amd.qwen3.ffn_moe import _fixed_capacity
+    from kappa_amd import _lib
+    from kappa_amd.qwen3 import moe_layer_config, moe_stages
+    from kappa_amd.qwen3.ffn_moe import _fixed_capacity, _moe_forward
 
     spec, cf, slots = case
     inp = make_inputs(spec)
@@ -516,13 +655,17 @@ def test_fixed_capacity_golden(dev, case):
     gold = np.load(f"tests/golden/{spec.name}.npz")
     assert cap == int(gold["capacity"]) == oracle.capacity_slots(spec.T, spec.K, spec.E, cf, slots)
     ref = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=spec.K,
-                         act_bf16=bf16, capacity=cap)  # fmt: skip
+                         act_bf16=bf16, impl="fixed_capacity", capacity=cap)  # fmt: skip
     # dispatch stage: inv carries -1 exactly for the dropped assignments
     rt = moe_stages.route(x, r, num_experts=spec.E, k=spec.K)
     dp = moe_stages.dispatch(rt["idx"], rt["hist"], num_experts=spec.E, capacity=cap)
     np.testing.assert_array_equal(dp["inv"].cpu().numpy(), ref["inv"])
     np.testing.assert_array_equal(dp["inv"].cpu().numpy(), gold["inv_cap"])
-    out = moe_swiglu_ffn(x.reshape(1, spec.T, spec.D), r, g, u, d, cfg=cfg).reshape(spec.T, spec.D)
+    fam = _lib.KERNELS_AUTO if kernels == "auto" else _lib.KERNELS_GROUPED
+    out = _moe_forward(
+        x.reshape(1, spec.T, spec.D), r, g, u, d, num_experts=spec.E, num_experts_per_tok=spec.K,
+        impl="fixed_capacity", decode_threshold=64, packed=None, capacity=cap, kernels=fam,
+    ).reshape(spec.T, spec.D)  # fmt: skip
     check_out(out.float().cpu().numpy(), ref["out"], bf16)
     check_out(out.float().cpu().numpy(), gold["out"], bf16, "vs golden")
 
@@ -531,11 +674,10 @@ def test_fixed_capacity_golden(dev, case):
 def test_30b_fixed_capacity(dev, l30, T, cf):
     """30B-A3B W8 layer with token dropping at decode and prefill sizes (sampled
     tokens against the oracle); every token's kept experts match the slot rule."""
-    from kappa_amd.qwen3 import moe_layer_config, moe_stages, moe_swiglu_ffn
+    from kappa_amd.qwen3 import moe_stages, moe_swiglu_ffn
     from kappa_amd.qwen3.ffn_moe import _fixed_capacity
 
-    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I,
-                           moe_impl="fixed_capacity", moe_capacity_factor=cf)  # fmt: skip
+    cfg = layer_cfg(l30, "fixed_capacity", moe_capacity_factor=cf)
     cap = _fixed_capacity(cfg, T)
     x = make_x(T, l30.D, seed=700 + T)
     r, d = _route_and_dispatch(x, l30.router, l30.E, l30.K)
@@ -549,7 +691,8 @@ def test_30b_fixed_capacity(dev, l30, T, cf):
     toks = np.unique(np.concatenate([rng.choice(T, size=min(32, T), replace=False), [0, T - 1]]))
     rows_t = np.repeat(toks, l30.K)
     rows_e = idx[toks].reshape(-1)
-    _, yo = oracle_rows(oracle, xn, rows_t, rows_e, l30.host())
+    _, yo = oracle_rows(oracle, xn, rows_t, rows_e, l30.host(), impl="fixed_capacity")
     kept = inv_cap.reshape(T, l30.K)[toks].reshape(-1)
-    ref = oracle.combine(yo, np.where(kept >= 0, np.arange(len(rows_t)), -1).astype(np.int32), w[toks], True)
+    ref = oracle.combine(yo, np.where(kept >= 0, np.arange(len(rows_t)), -1).astype(np.int32), w[toks], True,
+                         impl="fixed_capacity")  # fmt: skip
     check_out(bf16_np(out.reshape(T, l30.D))[toks], ref, True, "out rows")

@@ -101,3 +101,107 @@ def test_block_api_mirrors_the_moe_errors_and_rejects_cpu_tensors():
         rms_norm(x, scale)
     with pytest.raises(ValueError, match="out_dtype"):
         rms_norm(x, scale, out_dtype=torch.float16)
+
+
+def test_gather_program_rejects_per_channel_scales():
+    """moe_take_dequant (kappa/qwen3/quant.py:71-74) multiplies the gathered values by
+    the scale as stored; [E, 1, N] scales do not broadcast there, so per-channel W8 runs
+    on the ragged path (threshold 0 for decode batches) or fixed_capacity."""
+    x, r, g, u, d = args()
+    qc = [Q8Weight(torch.zeros(8, 16, 32, dtype=torch.int8), torch.ones(8, 1, 32)) for _ in range(2)]
+    qd = Q8Weight(torch.zeros(8, 32, 16, dtype=torch.int8), torch.ones(8, 1, 16))
+    with pytest.raises(ValueError, match="gather_einsum takes one scale per tensor"):
+        moe_swiglu_ffn(x, r, *qc, qd, cfg=cfg())
+    # ragged_jax at T <= threshold runs the gather program too (kappa/qwen3/ffn_moe.py:219-223)
+    with pytest.raises(ValueError, match="gather_einsum takes one scale per tensor"):
+        moe_swiglu_ffn(x, r, *qc, qd, cfg=cfg(moe_impl="ragged_jax"))
+    # the ragged program (above the threshold) and fixed_capacity accept them: the call
+    # gets as far as the device check
+    for c in (cfg(moe_impl="ragged_jax", moe_ragged_decode_token_threshold=0), cfg(moe_impl="fixed_capacity")):
+        with pytest.raises(ValueError, match="HIP device"):
+            moe_swiglu_ffn(x, r, *qc, qd, cfg=c)
+    # one scale per tensor is the gather path's own format
+    qt = [Q8Weight(w.values, torch.tensor(0.5)) for w in (*qc, qd)]
+    with pytest.raises(ValueError, match="HIP device"):
+        moe_swiglu_ffn(x, r, *qt, cfg=cfg())
+
+
+def test_packed_argument_must_match_the_layer():
+    from kappa_amd import _lib
+    from kappa_amd.qwen3 import PackedExperts
+
+    x, r, g, u, d = args()
+    t = torch.zeros(1)
+    c = cfg(moe_impl="ragged_jax", moe_ragged_decode_token_threshold=0)
+    for E, D, I in ((16, 16, 32), (8, 32, 32), (8, 16, 64)):
+        p = PackedExperts(t, t, t, t, D, I, E, _lib.SCALE_CHANNEL)
+        with pytest.raises(ValueError, match="packed experts hold"):
+            moe_swiglu_ffn(x, r, g, u, d, cfg=c, packed=p)
+    with pytest.raises(ValueError, match="PackedExperts"):
+        moe_swiglu_ffn(x, r, g, u, d, cfg=c, packed=(t, t, t, t))
+
+
+class _FakePack:
+    pass
+
+
+@pytest.fixture
+def pack_cache(monkeypatch):
+    """A fresh pack cache whose prepack step is a stand-in (no device needed)."""
+    from kappa_amd.qwen3 import ffn_moe
+
+    monkeypatch.setattr(ffn_moe, "prepack_moe_experts", lambda g, u, d: _FakePack())
+    return ffn_moe._PackCache()
+
+
+def _layer(seed):
+    gen = torch.Generator().manual_seed(seed)
+
+    def q(*shape):
+        return Q8Weight(torch.randint(-128, 127, shape, generator=gen, dtype=torch.int8), torch.rand(shape[0], 1,
+                                                                                                      shape[2]))
+
+    return q(4, 16, 8), q(4, 16, 8), q(4, 8, 16)
+
+
+def test_pack_cache_holds_a_whole_model_and_does_not_repack(pack_cache):
+    layers = [_layer(s) for s in range(48)]
+    first = [pack_cache.get(*lw) for lw in layers]
+    assert pack_cache.packs == 48 and len(pack_cache) == 48
+    second = [pack_cache.get(*lw) for lw in layers]
+    assert pack_cache.packs == 48
+    assert all(a is b for a, b in zip(first, second))
+
+
+def test_pack_cache_entry_dies_with_its_weights(pack_cache):
+    import gc
+
+    lw = _layer(0)
+    p0 = pack_cache.get(*lw)
+    assert len(pack_cache) == 1
+    del lw
+    gc.collect()
+    assert len(pack_cache) == 0, "a freed source must drop its entry"
+    # a new layer, even one that reuses the freed memory, misses and is packed anew
+    lw2 = _layer(1)
+    p1 = pack_cache.get(*lw2)
+    assert p1 is not p0 and pack_cache.packs == 2
+
+
+def test_pack_cache_misses_after_an_in_place_write(pack_cache):
+    lw = _layer(2)
+    p0 = pack_cache.get(*lw)
+    lw[1].values.add_(1)  # bumps the tensor's version
+    p1 = pack_cache.get(*lw)
+    assert p1 is not p0 and pack_cache.packs == 2
+    assert pack_cache.get(*lw) is p1
+
+
+def test_pack_cache_keys_on_identity_not_address(pack_cache):
+    # two layers whose tensors share storage (views of one buffer) are still two entries
+    base = _layer(3)
+    alias = tuple(Q8Weight(w.values.view(w.values.shape), w.scale.view(w.scale.shape)) for w in base)
+    assert all(a.values.data_ptr() == b.values.data_ptr() for a, b in zip(alias, base))
+    pa = pack_cache.get(*base)
+    pb = pack_cache.get(*alias)
+    assert pa is not pb and pack_cache.packs == 2

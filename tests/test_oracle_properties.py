@@ -167,13 +167,20 @@ def _dense_swiglu64(x, wg, wu, wd, bf16):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-def test_single_expert_reduces_to_dense_swiglu(bf16):
+@pytest.mark.parametrize("impl", ["gather_einsum", "ragged"])
+def test_single_expert_reduces_to_dense_swiglu(bf16, impl):
+    # E = 1, K = 1: the weight is exactly 1 and the layer is the dense swiglu_ffn
+    # (kappa/qwen3/ffn.py:12-22) with the impl's weight dtype: the gather path casts
+    # the weights to x.dtype, the ragged path computes in f32 and rounds only y
     spec = Spec("e1", T=9, D=64, E=1, K=1, I=48, act="bf16" if bf16 else "f32", weights="f32", router="f32")
     inp = make_inputs(spec)
-    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=1, act_bf16=bf16)
+    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=1, act_bf16=bf16, impl=impl)
     np.testing.assert_array_equal(r["w"], np.ones((9, 1), np.float32))
-    rnd = torch_bf16 if bf16 else (lambda a: a)
-    ref = _dense_swiglu64(inp["x"], rnd(inp["gate"][0]), rnd(inp["up"][0]), rnd(inp["down"][0]), bf16)
+    act_w = bf16 and impl == "gather_einsum"
+    rnd = torch_bf16 if act_w else (lambda a: a)
+    ref = _dense_swiglu64(inp["x"], rnd(inp["gate"][0]), rnd(inp["up"][0]), rnd(inp["down"][0]), act_w)
+    if bf16:
+        ref = torch_bf16(ref)
     tol = 2.0**-7 if bf16 else 1e-5
     assert np.all(np.abs(r["out"] - ref) <= tol * np.abs(ref).max())
 
@@ -183,7 +190,8 @@ def test_identical_experts_give_ffn_times_weight_sum():
     inp = make_inputs(spec)
     for n in ("gate", "up", "down"):
         inp[n] = np.repeat(inp[n][:1], 6, axis=0)
-    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=3, act_bf16=False)
+    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=3, act_bf16=False,
+                       impl="gather_einsum")  # fmt: skip
     ffn = _dense_swiglu64(inp["x"], inp["gate"][0], inp["up"][0], inp["down"][0], False)
     ref = ffn * r["w"].sum(-1, keepdims=True)
     np.testing.assert_allclose(r["out"], ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
@@ -192,7 +200,7 @@ def test_identical_experts_give_ffn_times_weight_sum():
 def test_k_equals_e_is_a_dense_softmax_mixture():
     spec = Spec("dense", T=5, D=32, E=4, K=4, I=16, act="f32", weights="f32", router="f32", x_std=1.0, r_std=0.5)
     inp = make_inputs(spec)
-    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=4, act_bf16=False)
+    r = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=4, act_bf16=False, impl="ragged")
     lg = inp["x"].astype(np.float64) @ inp["router"].astype(np.float64)
     p = np.exp(lg - lg.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
@@ -202,8 +210,14 @@ def test_k_equals_e_is_a_dense_softmax_mixture():
     np.testing.assert_allclose(r["out"], ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
 
 
+def _sigmoid32(g):
+    g = np.asarray(g, np.float32)
+    return (np.float32(1.0) / (np.float32(1.0) + np.exp(-g))).astype(np.float32)
+
+
 def test_dequant_rounds_scale_first_in_bf16():
-    # one expert, one row: y must use bf16(q * bf16(s)), not q * s
+    # one expert, one row: the gather path uses bf16(q * bf16(s)) (kappa/qwen3/quant.py:74),
+    # and h = bf16(bf16(g * bf16(sigmoid(g))) * u) (jax.nn.silu(g) * u in bf16)
     rng = np.random.default_rng(9)
     D, I = 64, 16
     x = bf16_rne(rng.standard_normal((1, D)).astype(np.float32))
@@ -211,25 +225,60 @@ def test_dequant_rounds_scale_first_in_bf16():
     s = np.full((1, 1, I), 0.0123456, np.float32)
     off = np.array([0, 1], np.int32)
     st = np.array([0], np.int32)
-    h, y = oracle.expert_ffn(x, off, st, (q, s), (q, s), (q.transpose(0, 2, 1).copy(), s[:, :, :1].repeat(D, 2)), True)
+    down = (q.transpose(0, 2, 1).copy(), s[:, :, :1].repeat(D, 2))
+    h, y = oracle.expert_ffn(x, off, st, (q, s), (q, s), down, True, impl="gather_einsum")
     w_deq = torch_bf16(q[0].astype(np.float32) * torch_bf16(s[0]))
     g = torch_bf16(x.astype(np.float64) @ w_deq.astype(np.float64))
-    np.testing.assert_array_equal(h, torch_bf16(g / (1 + np.exp(-g.astype(np.float64))) * g))
+    np.testing.assert_array_equal(h, torch_bf16(torch_bf16(g * torch_bf16(_sigmoid32(g))) * g))
     w_plain = q[0].astype(np.float32) * s[0]
     g2 = torch_bf16(x.astype(np.float64) @ w_plain.astype(np.float64))
     assert np.any(g2 != g), "scale rounding must matter for this input"
+    # the ragged path dequantises in f32 with the unrounded scale and keeps g, u and h
+    # in f32 (kappa/qwen3/ffn_moe.py:202-209); only y is rounded to bf16 (:213)
+    hr, yr = oracle.expert_ffn(x, off, st, (q, s), (q, s), down, True, impl="ragged")
+    gr = (x.astype(np.float64) @ w_plain.astype(np.float64)).astype(np.float32)
+    assert np.all(np.abs(hr - gr * _sigmoid32(gr) * gr) <= 1e-5 * np.abs(hr).max())
+    assert np.any(torch_bf16(hr) != hr), "ragged h must not be rounded to bf16"
+    yr64 = hr.astype(np.float64) @ (q[0].T.astype(np.float64) * np.float64(s[0, 0, 0]))
+    assert np.all(np.abs(yr - torch_bf16(yr64)) <= 2.0**-8 * np.abs(yr64) + 1e-30)
+
+
+@pytest.mark.parametrize("impl", ["gather_einsum", "ragged", "fixed_capacity"])
+def test_combine_rounding_points(impl):
+    # y * w rounded to bf16 for every impl; gather sums the products in f32 and rounds
+    # once (jnp.sum, kappa/qwen3/ffn_moe.py:103); ragged and fixed_capacity add them into
+    # a bf16 buffer, rounding after every add (.at[].add, :157, :215)
+    y = np.array([[1.0], [2.0**-8], [2.0**-8]], np.float32)  # three y rows of one column
+    inv = np.array([0, 1, 2], np.int32)
+    w = np.array([[1.0, 1.0, 1.0]], np.float32)
+    out = oracle.combine(y, inv, w, True, impl=impl)
+    # 1 + 2^-8 rounds to 1 in bf16 (a tie to even), twice; in f32 the sum is 1 + 2^-7 exactly
+    assert out[0, 0] == (np.float32(1.0 + 2.0**-7) if impl == "gather_einsum" else np.float32(1.0))
+    # the product is rounded before it is added: (1 + 2^-7)^2 = 1 + 2^-6 + 2^-14 -> 1 + 2^-6;
+    # plus 2^-8 that is a tie, which rounds to 1 + 2^-6. With the exact product the sum lies
+    # above the tie and rounds up to 1 + 2^-6 + 2^-7.
+    y2 = np.array([[1.0 + 2.0**-7], [2.0**-8]], np.float32)
+    w2 = np.array([[1.0 + 2.0**-7, 1.0]], np.float32)
+    got = oracle.combine(y2, np.array([0, 1], np.int32), w2, True, impl=impl)[0, 0]
+    assert got == np.float32(1.0 + 2.0**-6)
 
 
 def test_per_tensor_equals_per_channel_with_equal_scales():
     spec = Spec("pt", T=16, D=128, E=8, K=2, I=64, weights="w8t", scale_dtype="f32", base_seed=70)
     inp = make_inputs(spec)
-    a = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=2, act_bf16=True)
+    a = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=2, act_bf16=True, impl="ragged")
+    ag = oracle.forward(inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"], k=2, act_bf16=True,
+                        impl="gather_einsum")  # fmt: skip
     chan = {}
     for n, N in (("gate", 64), ("up", 64), ("down", 128)):
         q, s = inp[n]
         chan[n] = (q, np.full((8, 1, N), s, np.float32))
-    b = oracle.forward(inp["x"], inp["router"], chan["gate"], chan["up"], chan["down"], k=2, act_bf16=True)
+    b = oracle.forward(inp["x"], inp["router"], chan["gate"], chan["up"], chan["down"], k=2, act_bf16=True,
+                       impl="ragged")  # fmt: skip
     np.testing.assert_array_equal(a["out"], b["out"])
+    bg = oracle.forward(inp["x"], inp["router"], chan["gate"], chan["up"], chan["down"], k=2, act_bf16=True,
+                        impl="gather_einsum")  # fmt: skip
+    np.testing.assert_array_equal(ag["out"], bg["out"])
 
 
 # --- quantiser (A7) ------------------------------------------------------------
@@ -316,11 +365,15 @@ def _tiny_block(seed, act_bf16):
 
 @pytest.mark.parametrize("act_bf16", [True, False])
 def test_capacity_at_or_above_largest_group_is_dropless(act_bf16):
+    # nothing dropped: _moe_fixed_capacity is then the x.dtype expert chain of the gather
+    # path (to_compute_dtype(., x.dtype), :146-152) with the scatter-add combine (:157)
     spec, inp = _tiny_block(0, act_bf16)
     args = (inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"])
-    a = oracle.forward(*args, k=spec.K, act_bf16=act_bf16)
-    b = oracle.forward(*args, k=spec.K, act_bf16=act_bf16, capacity=int(a["group_sizes"].max()))
-    np.testing.assert_array_equal(a["out"], b["out"])
+    a = oracle.forward(*args, k=spec.K, act_bf16=act_bf16, impl="gather_einsum")
+    cap = int(a["group_sizes"].max())
+    b = oracle.forward(*args, k=spec.K, act_bf16=act_bf16, impl="fixed_capacity", capacity=cap)
+    np.testing.assert_array_equal(b["y_sorted"], a["y_sorted"])
+    np.testing.assert_array_equal(b["out"], oracle.combine(a["y_sorted"], a["inv"], a["w"], act_bf16, impl="ragged"))
     assert np.all(b["inv"] >= 0)
 
 
@@ -329,12 +382,12 @@ def test_dropped_assignments_remove_exactly_their_term():
     removed: recomputed here with the dropless rows and a zero weight."""
     spec, inp = _tiny_block(1, False)
     args = (inp["x"], inp["router"], inp["gate"], inp["up"], inp["down"])
-    a = oracle.forward(*args, k=spec.K, act_bf16=False)
-    b = oracle.forward(*args, k=spec.K, act_bf16=False, capacity=2)
+    a = oracle.forward(*args, k=spec.K, act_bf16=False, impl="gather_einsum")
+    b = oracle.forward(*args, k=spec.K, act_bf16=False, impl="fixed_capacity", capacity=2)
     dropped = (b["inv"] < 0).reshape(spec.T, spec.K)
     assert dropped.any()
     w0 = np.where(dropped, np.float32(0.0), a["w"]).astype(np.float32)
-    ref = oracle.combine(a["y_sorted"], a["inv"], w0, False)
+    ref = oracle.combine(a["y_sorted"], a["inv"], w0, False, impl="fixed_capacity")
     np.testing.assert_allclose(b["out"], ref, rtol=0, atol=1e-7)
     # tokens with nothing dropped are bit-identical to the dropless output
     keep_all = ~dropped.any(axis=1)
@@ -404,10 +457,12 @@ def test_block_with_zero_norm_scale_returns_the_residual(act_bf16):
     router = (0.02 * rng.standard_normal((D, E))).astype(np.float32)
     gate, up = (0.02 * rng.standard_normal((2, E, D, I))).astype(np.float32)
     down = (0.02 * rng.standard_normal((E, I, D))).astype(np.float32)
-    r = oracle.forward_block(h, np.zeros(D, np.float32), router, gate, up, down, k=K, act_bf16=act_bf16)
+    r = oracle.forward_block(h, np.zeros(D, np.float32), router, gate, up, down, k=K, act_bf16=act_bf16,
+                             impl="gather_einsum")  # fmt: skip
     np.testing.assert_array_equal(r["idx"], np.tile(np.arange(K, dtype=np.int32), (T, 1)))
     np.testing.assert_array_equal(r["out"], h)
     # and with nonzero norm but zero down weights the block output is zero too
-    r2 = oracle.forward_block(h, np.ones(D, np.float32), router, gate, up, np.zeros_like(down), k=K, act_bf16=act_bf16)
+    r2 = oracle.forward_block(h, np.ones(D, np.float32), router, gate, up, np.zeros_like(down), k=K, act_bf16=act_bf16,
+                              impl="ragged")  # fmt: skip
     assert not np.any(r2["moe_out"])
     np.testing.assert_array_equal(r2["out"], h)
