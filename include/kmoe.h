@@ -173,6 +173,22 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
                          int32_t* topk_idx_out, void* topk_w_out, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* kmoe_forward without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. The workspace is a
+ * device array of KMOE_NOALLOC_SCRATCH_BYTES inside the library, one per GPU,
+ * held until the process ends; the call allocates and frees nothing. A desc
+ * whose kmoe_workspace_bytes exceeds it returns KMOE_ERR_WORKSPACE_TOO_SMALL
+ * (with bf16 activations and the ragged program, the 30B-A3B layer fits up to
+ * 272 tokens and the 235B-A22B layer up to 136).
+ * Every call on one GPU shares the array: calls that overlap on a GPU (other
+ * streams, other threads) race and must be serialised by the caller. */
+#define KMOE_NOALLOC_SCRATCH_BYTES (16u << 20)
+kmoe_status kmoe_forward_noalloc(const kmoe_desc* desc, const void* x, const kmoe_weight* router,
+                                 const kmoe_weight* gate, const kmoe_weight* up, const kmoe_weight* down,
+                                 const kmoe_packed_experts* packed, void* out, int32_t* topk_idx_out, void* topk_w_out,
+                                 void* stream);
+
 /* The MoE half of a Qwen3 MoE layer with the steps on either side of the
  * block fused in (kappa/qwen3/block.py:71-82, 153-164, 196-207):
  *   h2  = rms_norm(h, norm_scale, epsilon)        (kappa/qwen3/norms.py:10-16)

@@ -43,6 +43,9 @@ KERNELS_GROUPED = 2
 
 ABI_VERSION = 3
 
+# kmoe_forward_noalloc's workspace (KMOE_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 16 << 20
+
 # Every symbol include/kmoe.h declares.
 EXPORTS = (
     "kmoe_version",
@@ -53,6 +56,7 @@ EXPORTS = (
     "kmoe_workspace_bytes",
     "kmoe_prepack_bytes",
     "kmoe_forward",
+    "kmoe_forward_noalloc",
     "kmoe_forward_block",
     "kmoe_rms_norm",
     "kmoe_route",
@@ -142,6 +146,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.kmoe_prepack_bytes.argtypes = [_DP, ctypes.POINTER(KmoePackedSizes)]
     L.kmoe_forward.restype = ctypes.c_int
     L.kmoe_forward.argtypes = [_DP, _P, _WP, _WP, _WP, _WP, _PP, _P, _P, _P, _P, ctypes.c_size_t, _P]
+    L.kmoe_forward_noalloc.restype = ctypes.c_int
+    L.kmoe_forward_noalloc.argtypes = [_DP, _P, _WP, _WP, _WP, _WP, _PP, _P, _P, _P, _P]
     L.kmoe_route.restype = ctypes.c_int
     L.kmoe_forward_block.restype = ctypes.c_int
     L.kmoe_forward_block.argtypes = [

@@ -477,6 +477,64 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
                         reinterpret_cast<char*>(workspace), w, (hipStream_t)stream);
 }
 
+}  // extern "C"
+
+// The workspace of kmoe_forward_noalloc: a file-scope device array, one copy on
+// every GPU the library runs on, held until the process ends. In host code the
+// name is only a handle for hipGetSymbolAddress; kernels get the per-device
+// address it returns.
+static __device__ __align__(256) uint8_t scratch[KMOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The address of `scratch` on the current device, looked up once per device.
+kmoe_status scratch_on_current_device(char** out) {
+  int dev = -1;
+  KMOE_HIP(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(KMOE_ERR_UNSUPPORTED, "device %d is beyond the %d devices kmoe_forward_noalloc serves", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    KMOE_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = reinterpret_cast<char*>(g_scratch_ptr[dev]);
+  return KMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+kmoe_status kmoe_forward_noalloc(const kmoe_desc* desc, const void* x, const kmoe_weight* router,
+                                 const kmoe_weight* gate, const kmoe_weight* up, const kmoe_weight* down,
+                                 const kmoe_packed_experts* packed, void* out, int32_t* topk_idx_out, void* topk_w_out,
+                                 void* stream) {
+  KMOE_TRY(check_forward_args(desc, router, gate, up, down, packed));
+  if (desc->tokens > 0 && (!x || !out))
+    return fail(KMOE_ERR_INVALID_ARG, "kmoe_forward_noalloc: x and out must be non-NULL");
+  const Workspace w = layout(*desc);
+  if (w.total > (size_t)KMOE_NOALLOC_SCRATCH_BYTES)
+    return fail(KMOE_ERR_WORKSPACE_TOO_SMALL,
+                "kmoe_forward_noalloc: the call needs %zu bytes of workspace, beyond its %zu-byte scratch; use "
+                "kmoe_forward with a workspace",
+                w.total, (size_t)KMOE_NOALLOC_SCRATCH_BYTES);
+  KMOE_TRY(device_status());
+  if (desc->tokens == 0) return KMOE_OK;
+  char* base = nullptr;
+  KMOE_TRY(scratch_on_current_device(&base));
+  // every workspace buffer is written before it is read within a call, so the
+  // previous call's contents need no clearing
+  return forward_stages(desc, x, nullptr, router, gate, up, down, packed, out, topk_idx_out, topk_w_out, base, w,
+                        (hipStream_t)stream);
+}
+
 kmoe_status kmoe_rms_norm(const kmoe_desc* desc, const void* x, const void* scale, kmoe_dtype scale_dtype,
                           float epsilon, void* out, void* stream) {
   KMOE_TRY(check_desc(desc));

@@ -245,3 +245,23 @@ def test_block_and_norm_entry_points_validate_before_any_hip_call():
         assert L.kmoe_rms_norm(d, 1, 1, BF, 1e-6, 2, None) == _lib.ERR_NO_DEVICE
         st = L.kmoe_forward_block(d, 7, 1, BF, 1e-6, f, w, w, w, None, 9, None, None, 1, 1 << 40, None)
         assert st == _lib.ERR_NO_DEVICE
+
+
+def test_noalloc_entry_point_limits_before_any_hip_call():
+    """kmoe_forward_noalloc runs on a fixed scratch array: a call whose workspace does
+    not fit is refused before any HIP call; one that fits reaches the device check."""
+    L = _lib.lib()
+    w = weight()
+    f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
+    big = desc(T=4096, D=2048, E=128, K=8, I=768)
+    n = ctypes.c_size_t()
+    assert L.kmoe_workspace_bytes(big, ctypes.byref(n)) == _lib.OK and n.value > _lib.NOALLOC_SCRATCH_BYTES
+    st, msg = status_and_msg(L.kmoe_forward_noalloc(big, 1, f, w, w, w, None, 1, None, None, None))
+    assert st == _lib.ERR_WORKSPACE_TOO_SMALL and "scratch" in msg
+    fits = desc(T=272, D=2048, E=128, K=8, I=768)
+    assert L.kmoe_workspace_bytes(fits, ctypes.byref(n)) == _lib.OK and n.value <= _lib.NOALLOC_SCRATCH_BYTES
+    st, msg = status_and_msg(L.kmoe_forward_noalloc(fits, None, f, w, w, w, None, 1, None, None, None))
+    assert st == _lib.ERR_INVALID_ARG and "x and out" in msg
+    if not gpu_available():
+        st, msg = status_and_msg(L.kmoe_forward_noalloc(fits, 1, f, w, w, w, None, 1, None, None, None))
+        assert st == _lib.ERR_NO_DEVICE
