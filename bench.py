@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
-"""Benchmark: the Qwen3-30B-A3B W8 MoE layer on one MI355X.
+"""Benchmark: the Qwen3-30B-A3B W8 MoE layer on one MI355X, and the other
+workloads of the same metric.
 
-    python bench.py [--steps K] [--warmup W] [--tokens T] [--copies R] [--sweep]
+    python bench.py [--steps K] [--warmup W] [--copies R] [--quick] [--no-cpu-baseline]
     python bench.py --copy-calibration MIB   # plain device copies of MIB MiB (counter calibration)
 
 A step is one call of the whole MoE block (router, top-k, dispatch, SwiGLU
@@ -10,17 +11,27 @@ weights are resident in HBM before timing starts. To measure HBM rather than
 the 256 MB Infinity Cache, steps rotate over R independent weight copies
 (R x 604 MB) and R activation batches.
 
+The layers hold per-output-channel W8 weights, which the reference runs with
+its ragged program (moe_impl ragged_jax; decode threshold 0 for the decode
+batches): that is the program every timed call follows. The gather program
+(the reference default, per-tensor W8) is timed beside it at decode T=64.
+
 Prints ONE JSON line on stdout (logs go to stderr):
-  value        decode tokens/s at T (default 64) = T * steps / elapsed
-  roofline     the dominant decode kernel (gate/up + SwiGLU), HBM-bound:
-               algorithmic bytes per launch / mean launch time from HIP events
-  prefill      the 4096-token prefill chunk: tokens/s and the MFMA roofline
-               of its dominant kernel (the gate/up grouped GEMM), next to
-               hipBLASLt bf16 GEMMs of the same shapes (library_reference)
-  --sweep      also decode T in {1, 8, 32}, prefill T in {512, 2048}, and the
-               235B-A22B-shaped layer (decode T=16, prefill T=2048)
-  cpu_baseline the oracle (the C restatement of the reference algorithm),
-               OpenMP on this host's cores, on a bounded sample
+  value          decode tokens/s at T=64 (the headline workload)
+  roofline       the dominant decode kernel (gate/up + SwiGLU), HBM-bound:
+                 algorithmic bytes per launch / mean launch time from HIP events
+  decode         T in {1, 8, 32, 64}: us/step, tokens/s, layer HBM fraction,
+                 the gate/up kernel's time and HBM fraction
+  prefill        T in {512, 2048, 4096}: us/step, tokens/s, layer MFMA and HBM
+                 fractions; the MFMA roofline of the gate/up grouped GEMM at 4096
+  skew           the Zipf(1.2)-skewed router at T=4096 and T=64, with the share of
+                 assignments the 8 hottest experts receive
+  layer_235b     the 235B-A22B-shaped layer: decode T=16, prefill T=2048
+  gather_decode  the gather program on per-tensor W8 at T=64
+  block          h + block(rms_norm(h)) fused in one call vs the separate steps
+  cpu_baseline   the oracle (the C restatement of the reference programs),
+                 OpenMP on this host's cores, on bounded samples (decode T=64 and
+                 a T=512 prefill chunk)
 """
 
 from __future__ import annotations
@@ -49,7 +60,7 @@ def log(*a):
 class Bound:
     """One layer copy with every C struct prebuilt, so a step is one ctypes call."""
 
-    def __init__(self, layer, T, impl="ragged_jax", threshold=0):
+    def __init__(self, layer, T, impl="ragged_jax", threshold=0, router=None):
         import torch
 
         from kappa_amd import _lib
@@ -57,30 +68,24 @@ class Bound:
         from kappa_amd.qwen3.quant import weight_struct
 
         self.layer = layer
+        self.router = layer.router if router is None else router
         dev = layer.router.device
         self.T = T
-        # per-channel W8: the ragged program at every token count (ragged_jax, threshold 0)
         self.desc = _desc(T, layer.D, layer.E, layer.K, layer.I, torch.bfloat16, impl=impl, threshold=threshold)
-        self.r, self._kr = weight_struct(layer.router, dev, n_out=layer.E, n_groups=None, name="router")
+        self.r, self._kr = weight_struct(self.router, dev, n_out=layer.E, n_groups=None, name="router")
         self.g, self._kg = weight_struct(layer.gate, dev, n_out=layer.I, n_groups=layer.E, name="gate")
         self.u, self._ku = weight_struct(layer.up, dev, n_out=layer.I, n_groups=layer.E, name="up")
         self.d, self._kd = weight_struct(layer.down, dev, n_out=layer.D, n_groups=layer.E, name="down")
         self.packed = PACK_CACHE.get(layer.gate, layer.up, layer.down)
-        PACK_CACHE.clear()
         self.p = self.packed.struct()
         n = ctypes.c_size_t()
         _lib.check(_lib.lib().kmoe_workspace_bytes(self.desc, ctypes.byref(n)))
         self.ws = torch.empty(n.value, dtype=torch.uint8, device=dev)
 
 
-def make_copies(R, T, seed0=0):
-    from moe_cases import make_layer
-
-    return [Bound(make_layer("30b", seed=seed0 + i), T) for i in range(R)]
-
-
 def time_forward(bounds, xs, outs, steps, warmup):
-    """Whole-block steps through kmoe_forward; returns (seconds, per-step list unused)."""
+    """Whole-block steps through kmoe_forward, rotating over the weight copies;
+    seconds for `steps` steps between two HIP events on the launch stream."""
     import torch
 
     from kappa_amd import _lib
@@ -174,7 +179,7 @@ def time_gate_up(bounds, xs, steps, decode: bool):
     for i, b in enumerate(bounds):
         lay = b.layer
         x = xs[i % len(xs)]
-        r = moe_stages.route(x, lay.router, num_experts=lay.E, k=lay.K)
+        r = moe_stages.route(x, b.router, num_experts=lay.E, k=lay.K)
         dsp = moe_stages.dispatch(r["idx"], r["hist"], num_experts=lay.E)
         h = torch.empty((x.shape[0] * lay.K, 2 * lay.I), dtype=torch.bfloat16, device=x.device)  # hi, lo planes
         items.append((b, x, dsp, h))
@@ -197,7 +202,6 @@ def _gate_up_only(b, x, dsp, h, decode):
     import torch
 
     from kappa_amd import _lib
-
     from kappa_amd.qwen3.ffn_moe import _desc
 
     lay = b.layer
@@ -227,78 +231,141 @@ def measured_traffic(kernel: str, workload: str):
     return None
 
 
-def bench_235b(bounds, xs, outs, args, dev):
-    """The 235B-A22B-shaped W8 layer (D 4096, E 128, K 8, I 1536, ~2.4 GB of
-    int8 experts): decode T=16 (HBM fraction) and prefill T=2048 (MFMA
-    fraction), two weight copies in rotation. Frees the 30B copies first."""
+def active_experts(bounds, xs):
+    """Mean number of experts with at least one assignment (U), over the copies."""
     import torch
 
     from kappa_amd.qwen3 import moe_stages
-    from moe_cases import make_layer
 
-    bounds.clear()
-    xs.clear()
-    outs.clear()
-    torch.cuda.empty_cache()
-    log("bench: building 2 weight copies of the 235B-A22B W8 layer")
-    big = [make_layer("235b", seed=40 + i) for i in range(2)]
-    D, E, K, I = big[0].D, big[0].E, big[0].K, big[0].I
-    res = {}
-    for T, kind in ((16, "decode"), (2048, "prefill")):
-        bb = [Bound(layer, T) for layer in big]
-        g = torch.Generator(device=dev)
-        g.manual_seed(13)
-        xb = [torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(2)]
-        ob = [torch.empty(T, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-        steps = args.steps if kind == "decode" else max(10, args.steps // 5)
-        secs = time_forward(bb, xb, ob, steps, args.warmup if kind == "decode" else 10)
-        step_s = secs / steps
-        if kind == "decode":
-            us_ = [
-                int(torch.unique(moe_stages.route(x, b.layer.router, num_experts=E, k=K)["idx"]).numel())
-                for b, x in zip(bb, xb)
-            ]
-            U = sum(us_) / len(us_)
-            lb = U * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 4 * T * D
-            res["decode_T16"] = {
-                "us_per_step": step_s * 1e6,
-                "tokens_per_s": T / step_s,
-                "layer_hbm_gbs": lb / step_s / 1e9,
-                "layer_hbm_frac": lb / step_s / 1e9 / HBM_PEAK_GBS,
-                "active_experts": U,
-            }
-        else:
-            fl = 2.0 * T * K * 3 * D * I + 2.0 * T * D * E
-            lb = E * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 4 * T * D
-            res["prefill_T2048"] = {
-                "us_per_step": step_s * 1e6,
-                "tokens_per_s": T / step_s,
-                "layer_tflops": fl / step_s / 1e12,
-                "layer_mfma_frac": fl / step_s / 1e12 / BF16_PEAK_TFLOPS,
-                "layer_hbm_frac": lb / step_s / 1e9 / HBM_PEAK_GBS,
-            }
-        log(f"bench: 235B {kind} T={T}: {step_s * 1e6:.1f} us/step")
-        del bb, xb, ob
-    del big
-    torch.cuda.empty_cache()
+    us = []
+    for i, b in enumerate(bounds):
+        lay = b.layer
+        idx = moe_stages.route(xs[i % len(xs)], b.router, num_experts=lay.E, k=lay.K)["idx"]
+        us.append(int(torch.unique(idx).numel()))
+    return sum(us) / len(us)
+
+
+def hot_share(bounds, xs, top=8):
+    """Share of the assignments that the `top` most-chosen experts receive."""
+    import torch
+
+    from kappa_amd.qwen3 import moe_stages
+
+    b, x = bounds[0], xs[0]
+    lay = b.layer
+    idx = moe_stages.route(x, b.router, num_experts=lay.E, k=lay.K)["idx"]
+    counts = torch.bincount(idx.reshape(-1).long(), minlength=lay.E)
+    return float(torch.topk(counts, top).values.sum().item() / idx.numel())
+
+
+def decode_bytes(layer, T, U):
+    """Algorithmic HBM bytes of one layer call with U active experts."""
+    D, E, I = layer.D, layer.E, layer.I
+    return U * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 4 * T * D
+
+
+def prefill_flops(layer, T):
+    return 2.0 * T * layer.K * 3 * layer.D * layer.I + 2.0 * T * layer.D * layer.E
+
+
+def make_x_list(T, D, n, seed, dev, skew=False):
+    import torch
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    xs = [torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(n)]
+    if skew:
+        for x in xs:
+            x[:, 0] = 1.0
+    return xs
+
+
+def decode_point(layers, T, args, dev, router_fn=None, impl="ragged_jax", threshold=0, seed=7):
+    """us/step, tokens/s, layer HBM fraction and the gate/up kernel at decode size T."""
+    import torch
+
+    bounds = [Bound(lay, T, impl=impl, threshold=threshold, router=router_fn(lay) if router_fn else None)
+              for lay in layers]  # fmt: skip
+    xs = make_x_list(T, layers[0].D, len(layers), seed + T, dev, skew=router_fn is not None)
+    outs = [torch.empty(T, layers[0].D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    secs = time_forward(bounds, xs, outs, args.steps, args.warmup)
+    step_s = secs / args.steps
+    U = active_experts(bounds, xs)
+    lb = decode_bytes(layers[0], T, U)
+    res = {
+        "us_per_step": step_s * 1e6,
+        "tokens_per_s": T / step_s,
+        "layer_hbm_gbs": lb / step_s / 1e9,
+        "layer_hbm_frac": lb / step_s / 1e9 / HBM_PEAK_GBS,
+        "active_experts": U,
+    }
+    if impl == "ragged_jax":
+        gu_ms, _ = time_gate_up(bounds, xs, max(args.steps, 16), decode=True)
+        lay = layers[0]
+        gu_bytes = U * (2 * lay.D * lay.I + 2 * lay.I * 4) + T * lay.D * 2 + T * lay.K * lay.I * 4
+        res["gate_up_us"] = gu_ms * 1e3
+        res["gate_up_gbs"] = gu_bytes / (gu_ms * 1e-3) / 1e9
+        res["gate_up_hbm_frac"] = res["gate_up_gbs"] / HBM_PEAK_GBS
+        res["_gate_up_bytes"] = gu_bytes
+    if router_fn is not None:
+        res["hot8_share"] = hot_share(bounds, xs)
+    log(f"bench: decode T={T} ({impl}{', skewed' if router_fn else ''}): {res['us_per_step']:.1f} us/step, "
+        f"layer HBM {res['layer_hbm_frac']:.3f}")  # fmt: skip
     return res
 
 
-def library_reference(T, D, I, E, K, reps=20):
-    """hipBLASLt (torch.bmm / torch.mm, bf16) on the prefill expert shapes with
-    uniform routing, M = T*K/E rows per expert, bf16 weights (no int8
-    dequantisation, no gather, no SwiGLU): a vendor-library reference point
-    for the grouped GEMMs, not part of the block."""
+def prefill_point(layers, T, args, dev, router_fn=None, roofline=False, seed=11):
+    import torch
+
+    bounds = [Bound(lay, T, router=router_fn(lay) if router_fn else None) for lay in layers]
+    xs = make_x_list(T, layers[0].D, len(layers), seed + T, dev, skew=router_fn is not None)
+    outs = [torch.empty(T, layers[0].D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    steps = max(10, args.steps // 2)
+    secs = time_forward(bounds, xs, outs, steps, max(args.warmup, 3))
+    step_s = secs / steps
+    lay = layers[0]
+    fl = prefill_flops(lay, T)
+    lb = decode_bytes(lay, T, lay.E)  # every expert is active at these sizes
+    res = {
+        "us_per_step": step_s * 1e6,
+        "tokens_per_s": T / step_s,
+        "layer_tflops": fl / step_s / 1e12,
+        "layer_mfma_frac": fl / step_s / 1e12 / BF16_PEAK_TFLOPS,
+        "layer_hbm_frac": lb / step_s / 1e9 / HBM_PEAK_GBS,
+    }
+    if router_fn is not None:
+        res["hot8_share"] = hot_share(bounds, xs)
+    if roofline:
+        gms, _ = time_gate_up(bounds, xs, steps, decode=False)
+        flops_gu = 2.0 * T * lay.K * lay.D * 2 * lay.I
+        tf = flops_gu / (gms * 1e-3) / 1e12
+        res["roofline"] = {
+            "kernel": "k_gemm<true> (gate/up grouped GEMM + SwiGLU)",
+            "bound": "mfma",
+            "achieved": tf,
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": tf / BF16_PEAK_TFLOPS,
+            "traffic": measured_traffic("k_gemm_gateup", f"prefill_T{T}"),
+            "algorithmic_flops_per_launch": flops_gu,
+            "mean_launch_us": gms * 1e3,
+        }
+    log(f"bench: prefill T={T}{' (skewed)' if router_fn else ''}: {res['us_per_step']:.1f} us/step, "
+        f"MFMA {res['layer_mfma_frac']:.3f}")  # fmt: skip
+    return res
+
+
+def library_reference(T, D, I, E, K, reps=10):
+    """hipBLASLt (torch.bmm, bf16) on the prefill expert shapes with uniform
+    routing, M = T*K/E rows per expert, bf16 weights (no int8 conversion, no
+    gather, no SwiGLU): a vendor-library reference point for the grouped GEMMs,
+    not part of the block."""
     import torch
 
     dev = torch.device("cuda:0")
     M = T * K // E
     out = {}
-    for name, (bs, m, k, n) in (
-        ("gate_up_bmm", (E, M, D, 2 * I)),
-        ("down_bmm", (E, M, I, D)),
-        ("gate_up_one_gemm", (1, T * K, D, 2 * I)),
-    ):
+    for name, (bs, m, k, n) in (("gate_up_bmm", (E, M, D, 2 * I)), ("down_bmm", (E, M, I, D))):
         a = torch.randn(bs, m, k, device=dev).to(torch.bfloat16)
         b = torch.randn(bs, k, n, device=dev).to(torch.bfloat16).contiguous()
         for _ in range(3):
@@ -318,40 +385,53 @@ def library_reference(T, D, I, E, K, reps=20):
     return out
 
 
-def cpu_baseline(layer, T, budget_s=12.0, max_reps=20):
-    """Time the oracle (C, OpenMP) on the same workload; bounded sample."""
-    import numpy as np
-
-    import oracle
-
-    host = layer.host()
-    x = layer_x_host(T, layer.D)
-    threads = len(os.sched_getaffinity(0))
-    oracle.set_threads(threads)
-    oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True,
-                   impl="ragged")  # warm  # fmt: skip
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
-        t0 = time.perf_counter()
-        oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True,
-                       impl="ragged")  # fmt: skip
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    cpu = ""
+def _cpu_name():
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return ""
+
+
+def cpu_baseline(layer, T_decode, T_prefill, budget_s=10.0):
+    """The oracle (C, OpenMP) on the ragged program, on bounded samples of the same
+    workloads: full layer calls at decode T_decode, then at a prefill chunk
+    T_prefill (a per-expert GEMM loop, which is what the ragged program's
+    ragged_dot computes)."""
+    import oracle
+
+    host = layer.host()
+    threads = len(os.sched_getaffinity(0))
+    oracle.set_threads(threads)
+    res = {}
+    for kind, T, max_reps in (("decode", T_decode, 20), ("prefill", T_prefill, 5)):
+        x = layer_x_host(T, layer.D)
+        oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True,
+                       impl="ragged")  # warm  # fmt: skip
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
+            t0 = time.perf_counter()
+            oracle.forward(x, host["router"], host["gate"], host["up"], host["down"], k=layer.K, act_bf16=True,
+                           impl="ragged")  # fmt: skip
+            times.append(time.perf_counter() - t0)
+        res[kind] = (T, statistics.median(times), len(times))
+    Td, md, nd = res["decode"]
+    Tp, mp, npf = res["prefill"]
     return {
-        "value": T / med,
+        "value": Td / md,
         "unit": "tokens/s",
         "cores": oracle.get_threads(),
         "kind": "port",
-        "sample": f"{len(times)} full layer calls at T={T} (30B-A3B W8, bf16), median {med * 1e3:.1f} ms; CPU: {cpu}",
+        "sample": (f"{nd} full layer calls at decode T={Td} (30B-A3B W8, bf16, ragged program), median "
+                   f"{md * 1e3:.1f} ms; CPU: {_cpu_name()}"),  # fmt: skip
+        "prefill": {
+            "value": Tp / mp,
+            "unit": "tokens/s",
+            "sample": f"{npf} full layer calls at a prefill chunk of T={Tp}, median {mp * 1e3:.1f} ms",
+        },
     }
 
 
@@ -364,19 +444,36 @@ def layer_x_host(T, D, seed=99):
     return bf16_rne(rng.standard_normal((T, D)).astype(np.float32))
 
 
+def bench_235b(args, dev):
+    """The 235B-A22B-shaped W8 layer (D 4096, E 128, K 8, I 1536, ~2.4 GB of
+    int8 experts): decode T=16 (HBM fraction) and prefill T=2048 (MFMA
+    fraction), two weight copies in rotation."""
+    import torch
+
+    from moe_cases import make_layer
+
+    log("bench: building 2 weight copies of the 235B-A22B W8 layer")
+    big = [make_layer("235b", seed=40 + i) for i in range(2)]
+    res = {"decode_T16": decode_point(big, 16, args, dev), "prefill_T2048": prefill_point(big, 2048, args, dev)}
+    for v in res.values():
+        v.pop("_gate_up_bytes", None)
+    del big
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=30)
     # the first ~100 steps after the weight build run ~6% slower (clocks and
-    # caches settling); 200 untimed steps cost ~25 ms
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--tokens", type=int, default=64)
+    # caches settling); 100 untimed steps cost ~12 ms
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--copies", type=int, default=8)
-    ap.add_argument("--prefill-tokens", type=int, default=4096)
-    ap.add_argument("--sweep", action="store_true", help="also time decode T in {1, 8, 32} and prefill T in {512, 2048}")
+    ap.add_argument("--quick", action="store_true", help="only the 30B decode and prefill points")
+    ap.add_argument("--decode", default="1,8,32,64", help="decode token counts; the largest is the headline")
+    ap.add_argument("--prefill", default="512,2048,4096", help="prefill token counts ('' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument(
         "--copy-calibration",
         type=int,
@@ -408,42 +505,31 @@ def main():
         return
 
     from kappa_amd import _lib
+    from moe_cases import make_layer, skew_router
 
     _lib.lib()
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    T = args.tokens
     R = args.copies
     log(f"bench: building {R} weight copies of the 30B-A3B W8 layer")
-    bounds = make_copies(R, T)
-    lay0 = bounds[0].layer
+    layers = [make_layer("30b", seed=i) for i in range(R)]
+    lay0 = layers[0]
     D, E, K, I = lay0.D, lay0.E, lay0.K, lay0.I
-    g = torch.Generator(device=dev)
-    g.manual_seed(7)
-    xs = [torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16) for _ in range(R)]
-    outs = [torch.empty(T, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
 
-    log(f"bench: decode T={T}: {args.warmup} warmup + {args.steps} timed steps")
-    secs = time_forward(bounds, xs, outs, args.steps, args.warmup)
-    ms_step = secs * 1e3 / args.steps
-    tok_s = T * args.steps / secs
-    log(f"bench: decode T={T}: {ms_step * 1e3:.1f} us/step, {tok_s:.0f} tokens/s")
-
-    gu_ms, U = time_gate_up(bounds, xs, max(args.steps, 16), decode=True)
-    M = T * K
-    gu_bytes = U * (2 * D * I + 2 * I * 4) + T * D * 2 + M * I * 2
-    gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
-    layer_bytes = U * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 2 * (2 * T * D)
-    log(f"bench: gate/up kernel {gu_ms * 1e3:.1f} us, U={U:.1f}, {gu_gbs:.0f} GB/s")
+    # headline: the largest decode batch asked for (T=64 by default)
+    dall = sorted({int(v) for v in args.decode.split(",") if v})
+    T = dall[-1]
+    dh = decode_point(layers, T, args, dev)
+    gu_bytes = dh.pop("_gate_up_bytes")
     result = {
         "metric": METRIC,
-        "value": tok_s,
+        "value": dh["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_step,
+        "ms_per_step": dh["us_per_step"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -457,31 +543,43 @@ def main():
             "top_k": K,
             "intermediate": I,
             "weights": "int8 per-output-channel fp32 scales, quantised from N(0,0.02)",
+            "program": "moe_impl ragged_jax, decode threshold 0 (_moe_ragged rounding points)",
             "weight_copies_rotated": R,
         },
         "roofline": {
             "kernel": "k_gateup_decode",
             "bound": "hbm",
-            "achieved": gu_gbs,
+            "achieved": dh["gate_up_gbs"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": gu_gbs / HBM_PEAK_GBS,
+            "frac": dh["gate_up_hbm_frac"],
             "traffic": measured_traffic("k_gateup_decode", f"decode_T{T}"),
             "algorithmic_bytes_per_launch": gu_bytes,
-            "mean_launch_us": gu_ms * 1e3,
-            "active_experts": U,
+            "mean_launch_us": dh["gate_up_us"],
+            "active_experts": dh["active_experts"],
         },
-        "layer_hbm_gbs": layer_bytes / (ms_step * 1e-3) / 1e9,
+        "layer_hbm_gbs": dh["layer_hbm_gbs"],
+        "layer_hbm_frac": dh["layer_hbm_frac"],
     }
-    result["layer_hbm_frac"] = result["layer_hbm_gbs"] / HBM_PEAK_GBS
+    decode = {str(T): dh}
+    for Ts in dall[:-1]:
+        p = decode_point(layers, Ts, args, dev)
+        p.pop("_gate_up_bytes", None)
+        decode[str(Ts)] = p
+    result["decode"] = {str(k): decode[str(k)] for k in dall}
 
     # the steps either side of the block: rms_norm in, residual add out. The
     # fused call, the three separate calls and the bare MoE layer are timed in
     # interleaved rounds (the clock drifts over a run); medians are reported.
+    bounds = [Bound(lay, T) for lay in layers]
+    xs = make_x_list(T, D, R, 77, dev)
+    outs = [torch.empty(T, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
     scale = (1.0 + 0.1 * torch.randn(D, generator=g, device=dev)).to(torch.bfloat16)
     rounds = {"fused": [], "separate": [], "moe_only": []}
-    n_round = max(args.steps // 5, 5)
-    for _ in range(5):
+    n_round = max(args.steps // 3, 5)
+    for _ in range(3):
         rounds["fused"].append(time_block(bounds, xs, outs, scale, n_round, 2, fused=True) / n_round)
         rounds["separate"].append(time_block(bounds, xs, outs, scale, n_round, 2, fused=False) / n_round)
         rounds["moe_only"].append(time_forward(bounds, xs, outs, n_round, 2) / n_round)
@@ -491,96 +589,61 @@ def main():
         "fused_us_per_step": med["fused"],
         "separate_us_per_step": med["separate"],
         "moe_only_us_per_step": med["moe_only"],
-        "rounds": f"5 interleaved rounds of {n_round} steps, medians",
+        "rounds": f"3 interleaved rounds of {n_round} steps, medians",
     }
-    log(f"bench: block {result['block']}")
+    del bounds
 
-    if args.sweep:
-        sweep = {}
-        for Ts in (1, 8, 32):
-            bs = [Bound(b.layer, Ts) for b in bounds]
-            xs_s = [x[:Ts].contiguous() for x in xs]
-            o_s = [torch.empty(Ts, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-            s = time_forward(bs, xs_s, o_s, args.steps, args.warmup)
-            gms, Us = time_gate_up(bs, xs_s, max(args.steps, 16), decode=True)
-            gb = Us * (2 * D * I + 2 * I * 4) + Ts * D * 2 + Ts * K * I * 2
-            lb = Us * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 2 * (2 * Ts * D)
-            sweep[str(Ts)] = {
-                "tokens_per_s": Ts * args.steps / s,
-                "us_per_step": s * 1e6 / args.steps,
-                "layer_hbm_gbs": lb / (s / args.steps) / 1e9,
-                "gate_up_us": gms * 1e3,
-                "gate_up_gbs": gb / (gms * 1e-3) / 1e9,
-                "active_experts": Us,
-            }
-            log(f"bench: decode T={Ts}: {sweep[str(Ts)]}")
-        result["decode_sweep"] = sweep
-
-    if not args.no_prefill:
-        Tp = args.prefill_tokens
-        log(f"bench: prefill T={Tp}")
-        bp = [Bound(b.layer, Tp) for b in bounds[:2]]
-        gp = torch.Generator(device=dev)
-        gp.manual_seed(11)
-        xp = [torch.randn(Tp, D, generator=gp, device=dev).to(torch.bfloat16) for _ in range(2)]
-        op = [torch.empty(Tp, D, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-        psteps = max(10, args.steps // 5)
-        s = time_forward(bp, xp, op, psteps, 10)
-        gms, Up = time_gate_up(bp, xp, psteps, decode=False)
-        Mp = Tp * K
-        flops_gu = 2.0 * Mp * D * 2 * I
-        flops_layer = 2.0 * Tp * K * 3 * D * I + 2.0 * Tp * D * E
-        tf = flops_gu / (gms * 1e-3) / 1e12
+    # prefill chunks on two copies (the weights stream once per call; MFMA-bound at 4096)
+    pl = layers[:2]
+    prefill = {}
+    for Tp in sorted({int(v) for v in args.prefill.split(",") if v}):
+        prefill[str(Tp)] = prefill_point(pl, Tp, args, dev, roofline=(Tp == 4096))
+    if prefill:
+        top = prefill[str(max(int(k) for k in prefill))]
         result["prefill"] = {
-            "workload": f"qwen3-30b-a3b W8 MoE layer, prefill chunk T={Tp}",
-            "tokens_per_s": Tp * psteps / s,
-            "ms_per_step": s * 1e3 / psteps,
-            "layer_tflops": flops_layer / (s / psteps) / 1e12,
-            "layer_mfma_frac": flops_layer / (s / psteps) / 1e12 / BF16_PEAK_TFLOPS,
-            "roofline": {
-                "kernel": "k_gemm<true> (gate/up grouped GEMM + SwiGLU)",
-                "bound": "mfma",
-                "achieved": tf,
-                "peak": BF16_PEAK_TFLOPS,
-                "unit": "TFLOP/s",
-                "frac": tf / BF16_PEAK_TFLOPS,
-                "traffic": measured_traffic("k_gemm_gateup", f"prefill_T{Tp}"),
-                "algorithmic_flops_per_launch": flops_gu,
-                "mean_launch_us": gms * 1e3,
-            },
+            "workload": "qwen3-30b-a3b W8 MoE layer, prefill chunks (ragged program)",
+            "tokens_per_s": top["tokens_per_s"],
+            "ms_per_step": top["us_per_step"] / 1e3,
+            "layer_tflops": top["layer_tflops"],
+            "layer_mfma_frac": top["layer_mfma_frac"],
+            "roofline": top.pop("roofline", None),
+            "chunks": prefill,
         }
-        result["prefill"]["library_reference"] = library_reference(Tp, D, I, E, K)
-        if args.sweep:
-            # the other prefill chunk sizes: whole-layer tokens/s and MFMA fraction
-            psweep = {}
-            for Tq in (512, 2048):
-                bq = [Bound(b.layer, Tq) for b in bounds[:2]]
-                xq = [x_[:Tq].contiguous() for x_ in xp]
-                oq = [o_[:Tq] for o_ in op]
-                sq = time_forward(bq, xq, oq, psteps, 10)
-                fq = 2.0 * Tq * K * 3 * D * I + 2.0 * Tq * D * E
-                # every expert is active at these sizes: the weight stream bounds T=512
-                bq_ = E * (3 * D * I + 4 * (2 * I + D)) + 2 * D * E + 4 * Tq * D
-                psweep[str(Tq)] = {
-                    "tokens_per_s": Tq * psteps / sq,
-                    "us_per_step": sq * 1e6 / psteps,
-                    "layer_tflops": fq / (sq / psteps) / 1e12,
-                    "layer_mfma_frac": fq / (sq / psteps) / 1e12 / BF16_PEAK_TFLOPS,
-                    "layer_hbm_frac": bq_ / (sq / psteps) / 1e9 / HBM_PEAK_GBS,
-                }
-                log(f"bench: prefill T={Tq}: {psweep[str(Tq)]}")
-            result["prefill"]["sweep"] = psweep
-        log(f"bench: prefill {result['prefill']}")
+
+    if not args.quick:
+        # Zipf(1.2)-skewed routing: the bias enters through x[:, 0] = 1 and router row 0
+        skewed = {id(lay): skew_router(lay.router, lam=1.5) for lay in layers}
+
+        def sk(lay):
+            return skewed[id(lay)]
+
+        s64 = decode_point(layers, 64, args, dev, router_fn=sk)
+        s64.pop("_gate_up_bytes", None)
+        result["skew"] = {"decode_T64": s64, "prefill_T4096": prefill_point(pl, 4096, args, dev, router_fn=sk)}
+        del skewed
+        # the gather program (the reference's default) on per-tensor W8 at decode T=64
+        gl = [make_layer("30b", seed=100 + i, per_tensor=True) for i in range(min(R, 4))]
+        gd = decode_point(gl, 64, args, dev, impl="gather_einsum", threshold=64)
+        gd["program"] = "moe_impl gather_einsum, per-tensor W8 (bf16 scale)"
+        result["gather_decode_T64"] = gd
+        del gl
+        if "prefill" in result:
+            result["prefill"]["library_reference"] = library_reference(4096, D, I, E, K)
 
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")
-        result["cpu_baseline"] = cpu_baseline(bounds[0].layer, T)
+        result["cpu_baseline"] = cpu_baseline(lay0, 64, 512)
         log(f"bench: cpu {result['cpu_baseline']}")
     else:
         result["cpu_baseline"] = None
 
-    if args.sweep:
-        result["layer_235b"] = bench_235b(bounds, xs, outs, args, dev)
+    if not args.quick:
+        del layers, pl, lay0
+        from kappa_amd.qwen3.ffn_moe import PACK_CACHE
+
+        PACK_CACHE.clear()
+        torch.cuda.empty_cache()
+        result["layer_235b"] = bench_235b(args, dev)
     print(json.dumps(result), flush=True)
 
 

@@ -68,8 +68,11 @@ struct Act<uint16_t> {
 constexpr int kChainAct = 0;
 constexpr int kChainF32 = 1;
 
-// sigmoid(g) = 1 / (1 + exp(-g)) in f32 (jax.nn.sigmoid)
-__device__ __forceinline__ float sigmoid_f32(float g) { return 1.0f / (1.0f + expf(-g)); }
+// sigmoid(g) = 1 / (1 + exp(-g)) in f32 (jax.nn.sigmoid) with the hardware exp2
+// and reciprocal: within a few f32 ulps of the correctly rounded value, far
+// below the bf16 rounding that follows (kChainAct) or the output tolerance
+// (kChainF32); exp overflow gives 0 and underflow 1, as the exact form does.
+__device__ __forceinline__ float sigmoid_f32(float g) { return __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // jax.nn.silu(g) * u (kappa/qwen3/ffn_moe.py:101, 151, 209) with silu(g) = g * sigmoid(g):
 // each product rounded to the activation dtype when R rounds (bf16), else f32.

@@ -338,6 +338,12 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
                                                       const int8_t* __restrict__ w2, const float* __restrict__ s2,
                                                       uint16_t* __restrict__ y_sorted, int cap) {
   static_assert(!ALLROWS || !GUARD, "row groups: one batch per wave");
+  // Rows per 16-row MFMA tile: 16, or 8 for kChainF32, whose tile rows 0..7 carry
+  // the hi plane of 8 rows of h and tile rows 8..15 their lo plane; the two
+  // halves of the product are added at the end. A decode expert has a few rows,
+  // so the lo plane rides in tile rows that would otherwise be empty.
+  constexpr int RPT = CH == kChainF32 ? 8 : 16;
+  constexpr int RPG = RPT * kDecodeMaxRowBlocks;  // rows per group
   __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][kDecodeMaxRowBlocks][NCG][64];
   const int dt = blockIdx.x;  // NCG*16 output columns
   const int slot = blockIdx.y;
@@ -361,22 +367,27 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
   float sc[NCG];
 #pragma unroll
   for (int cg = 0; cg < NCG; ++cg) sc[cg] = chain_scale<CH>(s2[(size_t)e * D + (dt * NCG + cg) * 16 + (lane & 15)]);
-  // kChainF32: h rows hold the hi and lo planes (stride 2I)
-  const size_t hstride = CH == kChainF32 ? 2 * (size_t)I : (size_t)I;
   const int r0 = offsets[e];
   const int nrows = min(offsets[e + 1] - r0, cap);
   const int koff = 16 * (lane >> 4);
-  // ALLROWS: the expert's rows in groups of kDecodeMaxRowBlocks 16-row blocks,
-  // the weights of the wave's single load batch kept in registers
-  const int ngroups = ALLROWS ? (nrows + 16 * kDecodeMaxRowBlocks - 1) / (16 * kDecodeMaxRowBlocks) : 1;
+  // Groups of RPG rows: ALLROWS (one load batch per wave, kept in registers) and
+  // kChainF32 (32 rows per group) loop over them; a wave with several load
+  // batches loads its weights again for each group.
+  const bool multi = c1 - c0 > NB;
+  const int ngroups = (ALLROWS || CH == kChainF32) ? (nrows + RPG - 1) / RPG : 1;
   for (int grp = 0; grp < ngroups; ++grp) {
-    const int rbase = grp * 16 * kDecodeMaxRowBlocks;
-    const int nrb = min((nrows - rbase + 15) >> 4, kDecodeMaxRowBlocks);
+    const int rbase = grp * RPG;
+    const int nrb = min((nrows - rbase + RPT - 1) / RPT, kDecodeMaxRowBlocks);
     const uint16_t* hr[kDecodeMaxRowBlocks];
 #pragma unroll
     for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
-      const int row = rbase + rb * 16 + (lane & 15);
-      hr[rb] = row < nrows ? h_sorted + (size_t)(r0 + row) * hstride + koff : nullptr;
+      if (CH == kChainF32) {
+        const int row = rbase + rb * 8 + (lane & 7);
+        hr[rb] = row < nrows ? h_sorted + (size_t)(r0 + row) * 2 * I + ((lane >> 3) & 1) * I + koff : nullptr;
+      } else {
+        const int row = rbase + rb * 16 + (lane & 15);
+        hr[rb] = row < nrows ? h_sorted + (size_t)(r0 + row) * I + koff : nullptr;
+      }
     }
     floatx4 acc[kDecodeMaxRowBlocks][NCG];
 #pragma unroll
@@ -384,24 +395,21 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) acc[rb][cg] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int cb = c0; cb < c1; cb += NB) {
-      if (cb != c0) load_w(cb);
+      if (cb != c0 || (grp > 0 && multi)) load_w(cb);
 #pragma unroll
       for (int rb = 0; rb < kDecodeMaxRowBlocks; ++rb) {
         if (rb < nrb) {
-          constexpr int NP = CH == kChainF32 ? 2 : 1;  // h planes
-          uint4 a0[NP][NB], a1[NP][NB];
+          uint4 a0[NB], a1[NB];
 #pragma unroll
-          for (int pl = 0; pl < NP; ++pl)
-#pragma unroll
-            for (int i = 0; i < NB; ++i) {
-              a0[pl][i] = uint4{0, 0, 0, 0};
-              a1[pl][i] = uint4{0, 0, 0, 0};
-              if (hr[rb] && (!GUARD || cb + i < c1)) {
-                const uint4* ap = reinterpret_cast<const uint4*>(hr[rb] + pl * I + (cb + i) * 64);
-                a0[pl][i] = ap[0];
-                a1[pl][i] = ap[1];
-              }
+          for (int i = 0; i < NB; ++i) {
+            a0[i] = uint4{0, 0, 0, 0};
+            a1[i] = uint4{0, 0, 0, 0};
+            if (hr[rb] && (!GUARD || cb + i < c1)) {
+              const uint4* ap = reinterpret_cast<const uint4*>(hr[rb] + (cb + i) * 64);
+              a0[i] = ap[0];
+              a1[i] = ap[1];
             }
+          }
 #pragma unroll
           for (int i = 0; i < NB; ++i) {
             if (!GUARD || cb + i < c1) {
@@ -409,11 +417,8 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
               for (int cg = 0; cg < NCG; ++cg) {
                 bf16x8 b0, b1;
                 weights16<CH>(q[i][cg], sc[cg], b0, b1);
-#pragma unroll
-                for (int pl = 0; pl < NP; ++pl) {
-                  acc[rb][cg] = mfma16(as_bf16x8(a0[pl][i]), b0, acc[rb][cg]);
-                  acc[rb][cg] = mfma16(as_bf16x8(a1[pl][i]), b1, acc[rb][cg]);
-                }
+                acc[rb][cg] = mfma16(as_bf16x8(a0[i]), b0, acc[rb][cg]);
+                acc[rb][cg] = mfma16(as_bf16x8(a1[i]), b1, acc[rb][cg]);
               }
             }
           }
@@ -437,18 +442,30 @@ __global__ __launch_bounds__(512) void k_down_decode(int D, int I, int E, const 
           floatx4 v = acc[rb][cg];
 #pragma unroll
           for (int w = 0; w < WPB - 1; ++w) v += red[w][rb][cg][lane];
+          if (CH == kChainF32) {
+            // tile row r (lanes 0..31) is the hi half of row r, tile row r + 8
+            // (lanes 32..63) its lo half: y = (hi + lo) * s
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int row = rbase + rb * 16 + 4 * (lane >> 4) + j;
-            if (row < nrows)
-              y_sorted[(size_t)(r0 + row) * D + (dt * NCG + cg) * 16 + (lane & 15)] =
-                  f32_to_bf16_bits(CH == kChainF32 ? __fmul_rn(v[j], sc[cg]) : v[j]);
+            for (int j = 0; j < 4; ++j) {
+              const float lo = __shfl_down(v[j], 32, 64);
+              const int row = rbase + rb * 8 + 4 * (lane >> 4) + j;
+              if (lane < 32 && row < nrows)
+                y_sorted[(size_t)(r0 + row) * D + (dt * NCG + cg) * 16 + (lane & 15)] =
+                    f32_to_bf16_bits(__fmul_rn(v[j] + lo, sc[cg]));
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int row = rbase + rb * 16 + 4 * (lane >> 4) + j;
+              if (row < nrows)
+                y_sorted[(size_t)(r0 + row) * D + (dt * NCG + cg) * 16 + (lane & 15)] = f32_to_bf16_bits(v[j]);
+            }
           }
         }
       }
     }
     // the reduction stage is reused by the next group
-    if (ALLROWS) __syncthreads();
+    if (ngroups > 1) __syncthreads();
   }
 }
 
@@ -702,15 +719,19 @@ struct GemmLoads {
   float sc[4];              // their scales (column lane % 16)
 };
 
-// KC chunks of 64 along A's rows; the weights have KCW chunks, and chunk c of A
-// meets weight chunk c % KCW (kChainF32 down: A = [hi | lo], KC = 2 * KCW).
-template <bool GATEUP, int MT, bool NTB, int CH>
-__device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, int KC, int KCW, int wv, int rows,
-                                          int row0, int nt, const uint16_t* __restrict__ src,
-                                          uint16_t* __restrict__ dst, int Ndim) {
+// KCW weight chunks of 64 along the reduction. PL = 1: A chunk c meets weight
+// chunk c. PL = 2 (the kChainF32 down product): an A row is h's hi plane then
+// its lo plane (2 * KCW chunks); A chunk c is plane c & 1 of weight chunk
+// c >> 1, so each weight chunk is loaded and converted once and meets both
+// planes in two consecutive iterations.
+template <bool GATEUP, int MT, bool NTB, int CH, int PL>
+__device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, int KCW, int wv, int rows, int row0,
+                                          int nt, const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                          int Ndim) {
   const int lane = threadIdx.x & 63;
   const uint32_t lds0 = lds_addr(smem);
   const uint8_t* const bring = smem + kGemmNA * kGemmA;
+  const int KC = PL * KCW;  // A chunks
   floatx4 acc[MT][4];
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi)
@@ -719,42 +740,56 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
 
   auto issue_a = [&](int c) {
     const uint32_t st = lds0 + (uint32_t)((c & 1) * kGemmA + wv * kGemmAJ * 1024);
-    const uint16_t* abase = src + c * 64;
+    const uint16_t* abase = src + (PL == 2 ? (c & 1) * (KCW * 64) + (c >> 1) * 64 : c * 64);
 #pragma unroll
     for (int j = 0; j < kGemmAJ; ++j) dma16(gl.avoff[j], abase, st + j * 1024);
   };
-  auto issue_b = [&](int c) {
-    const uint32_t st = lds0 + (uint32_t)(kGemmNA * kGemmA + (c % kGemmNB) * kGemmB + wv * 4096);
-    const int cw = c < KCW ? c : c - KCW;
+  auto issue_b = [&](int b) {
+    const uint32_t st = lds0 + (uint32_t)(kGemmNA * kGemmA + (b % kGemmNB) * kGemmB + wv * 4096);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       if (NTB)
-        dma16_stream(lane * 16, gl.bsrc[g] + cw * 1024, st + g * 1024);
+        dma16_stream(lane * 16, gl.bsrc[g] + b * 1024, st + g * 1024);
       else
-        dma16(lane * 16, gl.bsrc[g] + cw * 1024, st + g * 1024);
+        dma16(lane * 16, gl.bsrc[g] + b * 1024, st + g * 1024);
     }
   };
 
-  // Issue order: B(0), A(0), B(1); then iteration c issues A(c+1), B(c+2) and
-  // at its end waits for A(c+1) and B(c+1) (only B(c+2) may be outstanding).
+  // PL = 1. Issue order: B(0), A(0), B(1); then iteration c issues A(c+1),
+  // B(c+2) and at its end waits for A(c+1) and B(c+1) (only B(c+2) may be
+  // outstanding).
+  // PL = 2. Issue order: B(0), A(0); iteration c issues A(c+1) and, when c is
+  // even, B(c/2 + 1); at its end it waits for A(c+1) (c even: B(c/2 + 1) may
+  // stay outstanding) or for everything (c odd: B((c+1)/2) is read next).
   issue_b(0);
   issue_a(0);
-  if (1 < KC) {
+  if (PL == 1 && 1 < KC) {
     issue_b(1);
     vm_barrier<kGemmBJ>();
   } else {
     vm_barrier<0>();
   }
+  bf16x8 lo[4], hi[4];
   for (int c = 0; c < KC; ++c) {
+    const int b = PL == 2 ? c >> 1 : c;
+    bool b_ahead = false;  // a weight chunk issued this iteration
     if (c + 1 < KC) issue_a(c + 1);
-    if (c + 2 < KC) issue_b(c + 2);
-    uint4 raw[4];
-    const uint8_t* bp = bring + (c % kGemmNB) * kGemmB + wv * 4096 + lane * 16;
+    if (PL == 1 && c + 2 < KC) {
+      issue_b(c + 2);
+      b_ahead = true;
+    }
+    if (PL == 2 && (c & 1) == 0 && b + 1 < KCW) {
+      issue_b(b + 1);
+      b_ahead = true;
+    }
+    if (PL == 1 || (c & 1) == 0) {
+      uint4 raw[4];
+      const uint8_t* bp = bring + (b % kGemmNB) * kGemmB + wv * 4096 + lane * 16;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) raw[g] = *reinterpret_cast<const uint4*>(bp + g * 1024);
-    bf16x8 lo[4], hi[4];
+      for (int g = 0; g < 4; ++g) raw[g] = *reinterpret_cast<const uint4*>(bp + g * 1024);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) weights16<CH>(raw[g], gl.sc[g], lo[g], hi[g]);
+      for (int g = 0; g < 4; ++g) weights16<CH>(raw[g], gl.sc[g], lo[g], hi[g]);
+    }
     const uint16_t* As = reinterpret_cast<const uint16_t*>(smem + (c & 1) * kGemmA);
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -767,7 +802,7 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
       }
     }
     if (c + 1 < KC) {
-      if (c + 2 < KC)
+      if (b_ahead)
         vm_barrier<kGemmBJ>();
       else
         vm_barrier<0>();
@@ -874,16 +909,16 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   // wave may start loading into the ring while another still reads tok
   asm volatile("" ::"v"(gl.sc[0]), "v"(gl.sc[1]), "v"(gl.sc[2]), "v"(gl.sc[3]));
   __syncthreads();
-  const int KC = Kdim >> 6;
+  constexpr int PL = !GATEUP && CH == kChainF32 ? 2 : 1;  // h planes of the down product
   const int nmt = (rows + 15) >> 4;
   if (nmt > 4)
-    gemm_tile<GATEUP, 8, NTB, CH>(smem, gl, KC, KCW, wv, rows, row0, nt, src, dst, Ndim);
+    gemm_tile<GATEUP, 8, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
   else if (nmt > 2)
-    gemm_tile<GATEUP, 4, NTB, CH>(smem, gl, KC, KCW, wv, rows, row0, nt, src, dst, Ndim);
+    gemm_tile<GATEUP, 4, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
   else if (nmt == 2)
-    gemm_tile<GATEUP, 2, NTB, CH>(smem, gl, KC, KCW, wv, rows, row0, nt, src, dst, Ndim);
+    gemm_tile<GATEUP, 2, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
   else
-    gemm_tile<GATEUP, 1, NTB, CH>(smem, gl, KC, KCW, wv, rows, row0, nt, src, dst, Ndim);
+    gemm_tile<GATEUP, 1, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
 }
 
 // ---------------------------------------------------------------------------
@@ -1116,7 +1151,7 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, in
   // kChainF32: an h row is its hi and lo planes (2I)
   constexpr int NP = CH == kChainF32 ? 2 : 1;
   extern __shared__ __attribute__((aligned(16))) uint16_t hrows[];  // [TPB*K][NP*I]
-  __shared__ float part[3][kDownCombineMaxRows][16];                // chains 0+1, 2, 3 of row 0
+  __shared__ float part[2][3][kDownCombineMaxRows][16];  // [hi, lo] x chains 0+1, 2, 3 of row 0
   __shared__ float scl[kDownCombineMaxRows][16];                    // kChainF32: the column scales
   const int dt = blockIdx.x, tid = threadIdx.x;
   const int lane = tid & 63, wv = tid >> 6;  // blockDim.x = 128 * TPB * K
@@ -1161,8 +1196,10 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, in
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const bool row0 = (lane & 15) == 0;
-    const int koff = 16 * (lane >> 4);
+    // the assignment's row is tile row 0; kChainF32 puts its lo plane in tile
+    // row 8, as k_down_decode does
+    const bool rowhi = (lane & 15) == 0, rowlo = CH == kChainF32 && (lane & 15) == 8;
+    const int koff = 16 * (lane >> 4) + (rowlo ? I : 0);
     floatx4 acc[2];
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
@@ -1172,30 +1209,27 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, in
 #pragma unroll
       for (int c = 0; c < KCMAX; ++c) {
         if (cl + c >= c0 && cl + c < c1) {
+          uint4 a0v = uint4{0, 0, 0, 0}, a1v = uint4{0, 0, 0, 0};
+          if (rowhi || rowlo) {
+            const uint4* ap = reinterpret_cast<const uint4*>(hr + (cl + c) * 64 + koff);
+            a0v = ap[0];
+            a1v = ap[1];
+          }
           bf16x8 b0, b1;
           weights16<CH>(q[c], sc, b0, b1);
-          // the planes in k_down_decode's order: hi then lo
-#pragma unroll
-          for (int pl = 0; pl < NP; ++pl) {
-            uint4 a0v = uint4{0, 0, 0, 0}, a1v = uint4{0, 0, 0, 0};
-            if (row0) {
-              const uint4* ap = reinterpret_cast<const uint4*>(hr + pl * I + (cl + c) * 64 + koff);
-              a0v = ap[0];
-              a1v = ap[1];
-            }
-            acc[rr] = mfma16(as_bf16x8(a0v), b0, acc[rr]);
-            acc[rr] = mfma16(as_bf16x8(a1v), b1, acc[rr]);
-          }
+          acc[rr] = mfma16(as_bf16x8(a0v), b0, acc[rr]);
+          acc[rr] = mfma16(as_bf16x8(a1v), b1, acc[rr]);
         }
       }
     }
-    // lanes 0..15 hold row 0, columns 0..15
-    if (lane < 16) {
+    // lanes 0..15 hold tile row 0 (columns 0..15), lanes 32..47 tile row 8
+    const int pl = lane >> 5;
+    if ((lane & 31) < 16 && (pl == 0 || CH == kChainF32)) {
       if (half == 0) {
-        part[0][m][lane] = acc[0][0] + acc[1][0];
+        part[pl][0][m][lane & 15] = acc[0][0] + acc[1][0];
       } else {
-        part[1][m][lane] = acc[0][0];
-        part[2][m][lane] = acc[1][0];
+        part[pl][1][m][lane & 15] = acc[0][0];
+        part[pl][2][m][lane & 15] = acc[1][0];
       }
     }
   }
@@ -1208,8 +1242,9 @@ __global__ __launch_bounds__(1024) void k_down_combine(int T, int K, int TPB, in
       // a dropped assignment (inv < 0, fixed_capacity) adds nothing
       if (j < K && cinv[j] >= 0) {
         const int mj = t * K + j;
-        float v = (part[0][mj][col] + part[1][mj][col]) + part[2][mj][col];
-        if (CH == kChainF32) v = __fmul_rn(v, scl[mj][col]);
+        float v = (part[0][0][mj][col] + part[0][1][mj][col]) + part[0][2][mj][col];
+        if (CH == kChainF32)
+          v = __fmul_rn(v + ((part[1][0][mj][col] + part[1][1][mj][col]) + part[1][2][mj][col]), scl[mj][col]);
         acc = combine_term<uint16_t, SCATTER>(acc, cw[j], round_bf16(v));
       }
     }
