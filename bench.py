@@ -116,6 +116,48 @@ def time_forward(bounds, xs, outs, steps, warmup):
     return t0.elapsed_time(t1) / 1e3
 
 
+def time_forward_graph(bounds, xs, outs, steps, warmup):
+    """The same steps captured once in a HIP graph (one step per weight copy, in
+    rotation) and replayed, as a serving loop runs a decode step: the host
+    launches nothing per step. Returns seconds per step."""
+    import torch
+
+    from kappa_amd import _lib
+
+    L = _lib.lib()
+    R = len(bounds)
+
+    def one_round(stream):
+        for i, b in enumerate(bounds):
+            st = L.kmoe_forward(
+                b.desc, xs[i % len(xs)].data_ptr(), b.r, b.g, b.u, b.d, b.p, outs[i % len(outs)].data_ptr(),
+                None, None, b.ws.data_ptr(), b.ws.numel(), stream,
+            )  # fmt: skip
+            if st:
+                _lib.check(st)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        one_round(side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        one_round(torch.cuda.current_stream().cuda_stream)
+    reps = max(1, steps // R)
+    for _ in range(max(1, warmup // R)):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / 1e3 / (reps * R)
+
+
 def time_block(bounds, hs, outs, scale, steps, warmup, fused: bool):
     """The MoE half of the layer, h + block(rms_norm(h)) (kappa/qwen3/block.py:196-207):
     fused = one kmoe_forward_block call; otherwise kmoe_rms_norm, kmoe_forward and a
@@ -299,6 +341,10 @@ def decode_point(layers, T, args, dev, router_fn=None, impl="ragged_jax", thresh
         "layer_hbm_frac": lb / step_s / 1e9 / HBM_PEAK_GBS,
         "active_experts": U,
     }
+    # the same steps replayed from a HIP graph (steps and warm-up rounded to whole rotations)
+    g_s = time_forward_graph(bounds, xs, outs, max(args.steps, 8 * len(bounds)), args.warmup)
+    res["graph_us_per_step"] = g_s * 1e6
+    res["graph_tokens_per_s"] = T / g_s
     if impl == "ragged_jax":
         gu_ms, _ = time_gate_up(bounds, xs, max(args.steps, 16), decode=True)
         lay = layers[0]
@@ -309,8 +355,8 @@ def decode_point(layers, T, args, dev, router_fn=None, impl="ragged_jax", thresh
         res["_gate_up_bytes"] = gu_bytes
     if router_fn is not None:
         res["hot8_share"] = hot_share(bounds, xs)
-    log(f"bench: decode T={T} ({impl}{', skewed' if router_fn else ''}): {res['us_per_step']:.1f} us/step, "
-        f"layer HBM {res['layer_hbm_frac']:.3f}")  # fmt: skip
+    log(f"bench: decode T={T} ({impl}{', skewed' if router_fn else ''}): {res['us_per_step']:.1f} us/step "
+        f"({res['graph_us_per_step']:.1f} from a graph), layer HBM {res['layer_hbm_frac']:.3f}")  # fmt: skip
     return res
 
 
