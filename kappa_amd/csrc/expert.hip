@@ -150,7 +150,12 @@ __device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
 
 // ---------------------------------------------------------------------------
 // Decode (T <= 64): one block per (active expert, 16-column group); the WPB
-// waves split the reduction axis and are summed in wave order through LDS.
+// waves split the reduction axis. The reduction is cut into eight fixed parts
+// (chunks [KC*k/8, KC*(k+1)/8), one MFMA chain each) summed as
+// (((p0 + p1) + (p2 + p3)) + (p4 + p5)) + (p6 + p7) whatever the wave count
+// (eight waves: one part each; four: two parts each, added in the wave), so
+// every shape of this kernel - and with it a token's h - is the same for any
+// batch of up to 128 tokens.
 // Each weight byte is read exactly once per call. A wave issues the weight
 // loads of a batch of NB 64-deep chunks (NB x 1 KB per operand in flight)
 // before anything else - they depend only on the expert - then finds its rows
@@ -175,11 +180,17 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
                                                         uint16_t* __restrict__ h_sorted, int cap) {
   static_assert(!DENSE || (MRB == 1 && !GUARD), "dense tiles: one row block, one batch per wave");
   static_assert(!ALLROWS || (!DENSE && !GUARD), "row groups: gathered rows, one batch per wave");
-  __shared__ floatx4 red[WPB > 1 ? WPB - 1 : 1][MRB][2][64];
+  static_assert(WPB == 8 || WPB == 4, "eight reduction parts over eight or four waves");
+  constexpr int PPW = 8 / WPB;  // reduction parts per wave
+  const int pslot = (threadIdx.x >> 6) == 0 ? WPB - 1 : (threadIdx.x >> 6) - 1;
+  // red[w - 1]: wave w's sum for the cross-wave reduction; with two parts per
+  // wave, slot pslot also holds the wave's first part while it runs the second
+  __shared__ floatx4 red[8 / WPB == 2 ? WPB : WPB - 1][MRB][2][64];
   __shared__ int srt[16];  // DENSE: the tokens of the expert's rows
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int IG = I >> 4, KC = D >> 6;
   const int c0 = (KC * wv) / WPB, c1 = (KC * (wv + 1)) / WPB;
+  const int csplit = (KC * (PPW * wv + 1)) / 8;  // PPW = 2: the wave's second part starts here
   const int koff = 16 * (lane >> 4);
   uint4 da0[DENSE ? NB : 1], da1[DENSE ? NB : 1];
   if (DENSE) {
@@ -234,14 +245,34 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
         xr[rb] = row < nrows ? x + (size_t)tok * D + koff : nullptr;
       }
     }
+    // ag/au: the current reduction part; with two parts per wave (PPW = 2) the
+    // first is set aside in the wave's LDS slot when the second starts and
+    // added to it at the end, p(2w) + p(2w+1)
     floatx4 ag[MRB], au[MRB];
 #pragma unroll
     for (int rb = 0; rb < MRB; ++rb) {
       ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
       au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
+    bool parked = false;  // a first part is in the slot (wave-uniform)
+    auto set_aside = [&](int rb) {
+      parked = true;
+      red[pslot][rb][0][lane] = ag[rb];
+      red[pslot][rb][1][lane] = au[rb];
+      ag[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      au[rb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    };
+    auto next_part = [&]() {
+#pragma unroll
+      for (int rb = 0; rb < MRB; ++rb)
+        if (rb < nrb) set_aside(rb);
+    };
+    // Two parts start on load-batch boundaries when NB divides KC / 8 (D = 2048,
+    // 4096), or (a row-group kernel's single batch) in its middle.
+    constexpr bool SPLIT_IN_BATCH = ALLROWS && PPW == 2;
     for (int cb = c0; cb < c1; cb += NB) {
       if (cb != c0) load_w(cb);
+      if (PPW == 2 && !SPLIT_IN_BATCH && cb == csplit) next_part();
 #pragma unroll
       for (int rb = 0; rb < MRB; ++rb) {
         if (rb < nrb) {
@@ -263,6 +294,7 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
           }
 #pragma unroll
           for (int i = 0; i < NB; ++i) {
+            if (SPLIT_IN_BATCH && i == NB / 2) set_aside(rb);
             if (!GUARD || cb + i < c1) {
               bf16x8 bg0, bg1, bu0, bu1;
               weights16<CH>(qg[i], sg, bg0, bg1);
@@ -273,6 +305,17 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
               au[rb] = mfma16(as_bf16x8(a1[i]), bu1, au[rb]);
             }
           }
+        }
+      }
+    }
+    // PPW = 2: the wave's pair sum p(2w) + p(2w+1) (its own slot, read back by
+    // the lanes that wrote it)
+    if (PPW == 2 && parked) {
+#pragma unroll
+      for (int rb = 0; rb < MRB; ++rb) {
+        if (rb < nrb) {
+          ag[rb] = red[pslot][rb][0][lane] + ag[rb];
+          au[rb] = red[pslot][rb][1][lane] + au[rb];
         }
       }
     }
@@ -291,10 +334,22 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
       for (int rb = 0; rb < MRB; ++rb) {
         if (rb >= nrb) break;
         floatx4 g = ag[rb], u = au[rb];
+        if (PPW == 1) {
+          // (((p0 + p1) + (p2 + p3)) + (p4 + p5)) + (p6 + p7), red[w - 1] = p(w)
+          g += red[0][rb][0][lane];
+          u += red[0][rb][1][lane];
 #pragma unroll
-        for (int w = 0; w < WPB - 1; ++w) {
-          g += red[w][rb][0][lane];
-          u += red[w][rb][1][lane];
+          for (int w = 1; w < WPB - 1; w += 2) {
+            g += red[w][rb][0][lane] + red[w + 1][rb][0][lane];
+            u += red[w][rb][1][lane] + red[w + 1][rb][1][lane];
+          }
+        } else {
+          // ((q0 + q1) + q2) + q3 with q(w) = p(2w) + p(2w+1), red[w - 1] = q(w)
+#pragma unroll
+          for (int w = 0; w < WPB - 1; ++w) {
+            g += red[w][rb][0][lane];
+            u += red[w][rb][1][lane];
+          }
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

@@ -425,16 +425,16 @@ def test_fused_down_combine_shapes(dev, l30, l30t, T, K, impl):
     assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
 
 
-@pytest.mark.parametrize("T", [1, 4, 8, 15, 63])
+@pytest.mark.parametrize("T", [1, 4, 8, 15, 16, 63, 64, 100, 127])
 def test_decode_batch_invariance(dev, l30, T):
-    """A token's output does not depend on the other tokens of the call: the
-    first T rows of a (T + 1)-token call equal the T-token call bit for bit.
-    The pairs cross the kernel-shape switches of the decode path that keep the
-    summation order (fused down + combine up to T * K = 32, the dense token
-    tile of the gate/up kernel up to T = 4, the one-block finish + dispatch up
-    to T = 4 and T = 16). Between T = 16 and 17 the
-    gate/up reduction goes from eight wave chains to four, a different
-    grouping of the same sum, so that pair is not bit-identical."""
+    """A token's output does not depend on the other tokens of the call, up to
+    128 tokens: the first T rows of a (T + 1)-token call equal the T-token call
+    bit for bit. The pairs cross every kernel-shape switch below the grouped
+    GEMMs: the fused down + combine (T * K <= 32), the dense token tile of the
+    gate/up kernel (T <= 4), the one-block router finish and dispatch (T <= 16),
+    eight against four gate/up waves (T = 16/17; both sum the same eight
+    reduction parts in the same order), and the row-group kernels (T = 64/65).
+    Above 128 tokens the grouped GEMMs sum in another order."""
     from kappa_amd.qwen3 import moe_swiglu_ffn
 
     cfg = layer_cfg(l30, "ragged")
