@@ -965,15 +965,34 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   asm volatile("" ::"v"(gl.sc[0]), "v"(gl.sc[1]), "v"(gl.sc[2]), "v"(gl.sc[3]));
   __syncthreads();
   constexpr int PL = !GATEUP && CH == kChainF32 ? 2 : 1;  // h planes of the down product
-  const int nmt = (rows + 15) >> 4;
-  if (nmt > 4)
-    gemm_tile<GATEUP, 8, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
-  else if (nmt > 2)
-    gemm_tile<GATEUP, 4, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
-  else if (nmt == 2)
-    gemm_tile<GATEUP, 2, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
-  else
-    gemm_tile<GATEUP, 1, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+  // as many 16-row MFMA tiles as the rows need (an expert's last row tile is
+  // usually partial)
+  switch ((rows + 15) >> 4) {
+    case 8:
+      gemm_tile<GATEUP, 8, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+    case 7:
+      gemm_tile<GATEUP, 7, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+    case 6:
+      gemm_tile<GATEUP, 6, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+    case 5:
+      gemm_tile<GATEUP, 5, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+    case 4:
+      gemm_tile<GATEUP, 4, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+    case 3:
+      gemm_tile<GATEUP, 3, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+    case 2:
+      gemm_tile<GATEUP, 2, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+    default:
+      gemm_tile<GATEUP, 1, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+  }
 }
 
 // ---------------------------------------------------------------------------
