@@ -383,6 +383,12 @@ kmoe_status check_forward_args(const kmoe_desc* desc, const kmoe_weight* router,
   return KMOE_OK;
 }
 
+kmoe_status forward_general(const kmoe_desc* desc, const void* x, const void* xin, const void* res,
+                            const kmoe_host::SliceNorm* norm, const kmoe_weight* router, const kmoe_weight* gate,
+                            const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed,
+                            void* out, char* base, const Workspace& w, int chain, bool scatter,
+                            const kmoe_host::DispatchOut& dout, hipStream_t st);
+
 // The stage sequence of moe_swiglu_ffn on x. With a norm, x is the residual
 // stream h: the block runs on h2 = rms_norm(h) (norm->h2, computed by the
 // split router at T <= 128, else by the norm kernel) and the combine adds the
@@ -395,13 +401,54 @@ kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host
   const void* xin = norm ? norm->h2 : x;  // the block's input, after the norm
   int32_t* tidx = reinterpret_cast<int32_t*>(base + w.topk_idx);
   float* tw = reinterpret_cast<float*>(base + w.topk_w);
-  int32_t* hist = reinterpret_cast<int32_t*>(base + w.hist);
-  int32_t* gs = reinterpret_cast<int32_t*>(base + w.group_sizes);
-  int32_t* off = reinterpret_cast<int32_t*>(base + w.offsets);
-  int32_t* act = reinterpret_cast<int32_t*>(base + w.active);
-  int32_t* stok = reinterpret_cast<int32_t*>(base + w.sorted_token);
-  int32_t* sexp = reinterpret_cast<int32_t*>(base + w.sorted_expert);
   int32_t* inv = reinterpret_cast<int32_t*>(base + w.inv);
+  void* hs = base + w.h_sorted;
+  const int chain = chain_of(*desc);
+  const bool scatter = scatter_of(*desc);
+  const kmoe_host::DispatchOut dout{reinterpret_cast<int32_t*>(base + w.group_sizes),
+                                    reinterpret_cast<int32_t*>(base + w.offsets),
+                                    reinterpret_cast<int32_t*>(base + w.active),
+                                    reinterpret_cast<int32_t*>(base + w.sorted_token),
+                                    reinterpret_cast<int32_t*>(base + w.sorted_expert), inv};
+  if (packed_ok(*desc, packed) && family_of(*desc) == kmoe_host::kFamilyDecode &&
+      kmoe_host::down_combine_fits(*desc, chain) && kmoe_host::gateup_routed_fits(*desc)) {
+    // up to four tokens: the router's slices, then the gate/up kernel that
+    // finishes the tokens and sorts their assignments itself, then the down
+    // projection with the combine
+    float* part = reinterpret_cast<float*>(base + w.route_part);
+    KMOE_HIP(kmoe_host::launch_route_slices(*desc, x, *router, part, st, norm), "route kernel");
+    KMOE_HIP(kmoe_host::launch_gateup_routed(*desc, chain, part, xin, *packed, hs, tidx, tw, dout, st),
+             "gate/up kernel");
+    KMOE_HIP(kmoe_host::launch_down_combine(*desc, chain, scatter, hs, tidx, inv, tw, *packed, out, st, res),
+             "down+combine kernel");
+  } else {
+    KMOE_TRY(forward_general(desc, x, xin, res, norm, router, gate, up, down, packed, out, base, w, chain, scatter,
+                             dout, st));
+  }
+  if (topk_idx_out)
+    KMOE_HIP(hipMemcpyAsync(topk_idx_out, tidx, sizeof(int32_t) * desc->tokens * desc->top_k,
+                            hipMemcpyDeviceToDevice, st),
+             "copy topk_idx");
+  if (topk_w_out) KMOE_HIP(kmoe_host::launch_topk_w_cast(*desc, tw, topk_w_out, st), "topk_w cast");
+  return KMOE_OK;
+}
+
+// The other sizes: router (with the dispatch sort at T <= 16), dispatch,
+// expert stages and combine.
+kmoe_status forward_general(const kmoe_desc* desc, const void* x, const void* xin, const void* res,
+                            const kmoe_host::SliceNorm* norm, const kmoe_weight* router, const kmoe_weight* gate,
+                            const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed,
+                            void* out, char* base, const Workspace& w, int chain, bool scatter,
+                            const kmoe_host::DispatchOut& dout, hipStream_t st) {
+  int32_t* tidx = reinterpret_cast<int32_t*>(base + w.topk_idx);
+  float* tw = reinterpret_cast<float*>(base + w.topk_w);
+  int32_t* hist = reinterpret_cast<int32_t*>(base + w.hist);
+  int32_t* gs = dout.group_sizes;
+  int32_t* off = dout.offsets;
+  int32_t* act = dout.active;
+  int32_t* stok = dout.sorted_token;
+  int32_t* sexp = dout.sorted_expert;
+  int32_t* inv = dout.inv;
   void* hs = base + w.h_sorted;
   void* ys = base + w.y_sorted;
   if (desc->tokens <= kmoe_host::kSplitRouterMaxTokens) {
@@ -409,7 +456,6 @@ kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host
     // running the dispatch sort itself at T <= 16); one 64-token chunk counts
     // itself in the dispatch, two need the chunk histograms first
     float* part = reinterpret_cast<float*>(base + w.route_part);
-    const kmoe_host::DispatchOut dout{gs, off, act, stok, sexp, inv};
     KMOE_HIP(kmoe_host::launch_route_split(*desc, x, *router, part, nullptr, tidx, tw, st, norm, &dout),
              "route kernels");
     if (desc->tokens > kmoe::kDispatchBlock) {
@@ -427,8 +473,6 @@ kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host
     KMOE_HIP(kmoe_host::launch_route(*desc, xin, *router, nullptr, tidx, tw, hist, st), "route kernels");
     KMOE_HIP(kmoe_host::launch_dispatch(*desc, tidx, hist, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
   }
-  const int chain = chain_of(*desc);
-  const bool scatter = scatter_of(*desc);
   if (packed_ok(*desc, packed) && family_of(*desc) == kmoe_host::kFamilyDecode &&
       kmoe_host::down_combine_fits(*desc, chain)) {
     // at most 32 assignments: the down projection and the combine in one kernel
@@ -441,11 +485,6 @@ kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host
                           up, down, packed, hs, ys, st));
     KMOE_HIP(kmoe_host::launch_combine(*desc, scatter, ys, inv, tw, out, st, res), "combine kernel");
   }
-  if (topk_idx_out)
-    KMOE_HIP(hipMemcpyAsync(topk_idx_out, tidx, sizeof(int32_t) * desc->tokens * desc->top_k,
-                            hipMemcpyDeviceToDevice, st),
-             "copy topk_idx");
-  if (topk_w_out) KMOE_HIP(kmoe_host::launch_topk_w_cast(*desc, tw, topk_w_out, st), "topk_w cast");
   return KMOE_OK;
 }
 

@@ -16,9 +16,11 @@
 // in sub-step s, for both operands, which matches the packed layout
 // [.., k/16, col, 16 k] where each lane's 16 bytes are one column's 16 k.
 #include <algorithm>
+#include <atomic>
 
 #include "common.h"
 #include "launch.h"
+#include "route_dev.h"
 
 namespace kmoe {
 
@@ -172,12 +174,13 @@ __device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
 // issued first, ahead of the expert lookup.
 // ---------------------------------------------------------------------------
 template <int WPB, int NB, bool GUARD, int MRB, bool DENSE, bool ALLROWS, int CH>
-__global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int E, const uint16_t* __restrict__ x,
-                                                        const int32_t* __restrict__ offsets,
-                                                        const int32_t* __restrict__ active,
-                                                        const int32_t* __restrict__ sorted_token,
-                                                        const int8_t* __restrict__ w13, const float* __restrict__ s13,
-                                                        uint16_t* __restrict__ h_sorted, int cap) {
+__device__ __forceinline__ void gateup_decode_body(int ig, int slot, int T, int D, int I, int E,
+                                                   const uint16_t* __restrict__ x,
+                                                   const int32_t* __restrict__ offsets,
+                                                   const int32_t* __restrict__ active,
+                                                   const int32_t* __restrict__ sorted_token,
+                                                   const int8_t* __restrict__ w13, const float* __restrict__ s13,
+                                                   uint16_t* __restrict__ h_sorted, int cap) {
   static_assert(!DENSE || (MRB == 1 && !GUARD), "dense tiles: one row block, one batch per wave");
   static_assert(!ALLROWS || (!DENSE && !GUARD), "row groups: gathered rows, one batch per wave");
   static_assert(WPB == 8 || WPB == 4, "eight reduction parts over eight or four waves");
@@ -206,8 +209,6 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
       }
     }
   }
-  const int ig = blockIdx.x;
-  const int slot = blockIdx.y;
   const int n_active = active[E];
   const int e = active[slot < E ? slot : 0];
   if (slot >= n_active) return;
@@ -380,6 +381,75 @@ __global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int 
     }
     // the reduction stage is reused by the next group
     if (ALLROWS) __syncthreads();
+  }
+}
+
+template <int WPB, int NB, bool GUARD, int MRB, bool DENSE, bool ALLROWS, int CH>
+__global__ __launch_bounds__(512) void k_gateup_decode(int T, int D, int I, int E, const uint16_t* __restrict__ x,
+                                                        const int32_t* __restrict__ offsets,
+                                                        const int32_t* __restrict__ active,
+                                                        const int32_t* __restrict__ sorted_token,
+                                                        const int8_t* __restrict__ w13, const float* __restrict__ s13,
+                                                        uint16_t* __restrict__ h_sorted, int cap) {
+  gateup_decode_body<WPB, NB, GUARD, MRB, DENSE, ALLROWS, CH>(blockIdx.x, blockIdx.y, T, D, I, E, x, offsets, active,
+                                                              sorted_token, w13, s13, h_sorted, cap);
+}
+
+// Decode with at most four tokens, whole-block call: the router's finish and
+// the dispatch sort run at the start of every gate/up block (each block
+// finishes the T tokens from the split router's group partials and sorts
+// their assignments into LDS, all blocks alike), so no kernel sits between
+// the router's slices and the expert products. Block 0 also writes the
+// selections, weights and dispatch arrays for the down + combine kernel.
+// The grid is at most one resident round of blocks; each block then runs the
+// (16-column group, active expert) items blockIdx.x, + gridDim.x, ..., so the
+// routing is paid once per block. The products are those of
+// k_gateup_decode's dense form.
+template <int EPL, int NB, int CH>
+__global__ __launch_bounds__(512) void k_gateup_routed(int T, int D, int I, int E, int K, int Q,
+                                                        const float* __restrict__ part, int out_bf16,
+                                                        const uint16_t* __restrict__ x,
+                                                        const int8_t* __restrict__ w13, const float* __restrict__ s13,
+                                                        uint16_t* __restrict__ h_sorted, int cap,
+                                                        int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
+                                                        int32_t* __restrict__ group_sizes, int32_t* __restrict__ offsets,
+                                                        int32_t* __restrict__ active,
+                                                        int32_t* __restrict__ sorted_token,
+                                                        int32_t* __restrict__ sorted_expert,
+                                                        int32_t* __restrict__ inv) {
+  constexpr int MT = 4 * kMaxTopK;  // T <= 4
+  __shared__ TopkLds tk[4];
+  __shared__ DispatchLds L;
+  __shared__ int32_t sel[MT], l_tidx[MT], l_stok[MT], l_sexp[MT], l_inv[MT];
+  __shared__ float l_tw[MT];
+  __shared__ int32_t l_gs[kMaxExperts], l_off[kMaxExperts + 1], l_act[kMaxExperts + 1];
+  const int w = threadIdx.x >> 6;
+  if (w < T) finish_token<EPL>(w, E, K, Q, part, nullptr, l_tidx, l_tw, out_bf16, sel, tk[w]);
+  __syncthreads();
+  dispatch_chunk(T, E, K, 0, 1, sel, nullptr, l_gs, l_off, l_act, l_stok, l_sexp, l_inv, cap, L);
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    const int M = T * K;
+    for (int i = threadIdx.x; i < M; i += blockDim.x) {
+      topk_idx[i] = l_tidx[i];
+      topk_w[i] = l_tw[i];
+      sorted_token[i] = l_stok[i];
+      sorted_expert[i] = l_sexp[i];
+      inv[i] = l_inv[i];
+    }
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) {
+      offsets[e] = l_off[e];
+      active[e] = l_act[e];
+      if (e < E) group_sizes[e] = l_gs[e];
+    }
+  }
+  const int IG = I >> 4;
+  const int n_items = IG * l_act[E];
+  for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
+    gateup_decode_body<8, NB, false, 1, true, false, CH>(it % IG, it / IG, T, D, I, E, x, l_off, l_act, l_stok, w13,
+                                                         s13, h_sorted, cap);
+    // the body's LDS reduction stage is reused by the next item
+    __syncthreads();
   }
 }
 
@@ -1634,6 +1704,78 @@ hipError_t launch_down_combine(const kmoe_desc& d, int chain, bool scatter, cons
   else
     down_combine_modes<12>(chain, scatter, grid, block, lds, st, T, K, TPB, D, I, hb, topk_idx, inv, topk_w, w2, s2,
                            ob, rb);
+  return hipGetLastError();
+}
+
+// Compute units of the current device (cached per device).
+static int cu_count() {
+  constexpr int kDevices = 64;
+  static std::atomic<int> cache[kDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+bool gateup_routed_fits(const kmoe_desc& d) {
+  return d.tokens >= 1 && d.tokens <= 4 && d.act_dtype == KMOE_DTYPE_BF16 &&
+         (d.hidden == 32 * 64 || d.hidden == 64 * 64) && d.intermediate % 16 == 0 && d.top_k >= 1 &&
+         d.top_k <= kmoe::kMaxTopK && d.num_experts <= kmoe::kMaxExperts;
+}
+
+template <int EPL, int CH>
+static void routed_launch(const kmoe_desc& d, int Q, const float* part, const uint16_t* xb, const int8_t* w13,
+                          const float* s13, uint16_t* hb, int32_t* tidx, float* tw, const DispatchOut& o,
+                          hipStream_t st) {
+  const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts, K = (int)d.top_k,
+            I = (int)d.intermediate;
+  // at most min(T*K, E) active experts; two blocks per CU are resident
+  const int items = (I / 16) * std::min(T * K, E);
+  const dim3 grid(std::min(items, 2 * cu_count()));
+  if (D == 32 * 64)
+    hipLaunchKernelGGL((k_gateup_routed<EPL, 4, CH>), grid, dim3(512), 0, st, T, D, I, E, K, Q, part, 1, xb, w13, s13,
+                       hb, capacity_of(d), tidx, tw, o.group_sizes, o.offsets, o.active, o.sorted_token,
+                       o.sorted_expert, o.inv);
+  else
+    hipLaunchKernelGGL((k_gateup_routed<EPL, 8, CH>), grid, dim3(512), 0, st, T, D, I, E, K, Q, part, 1, xb, w13, s13,
+                       hb, capacity_of(d), tidx, tw, o.group_sizes, o.offsets, o.active, o.sorted_token,
+                       o.sorted_expert, o.inv);
+}
+
+template <int CH>
+static void routed_epl(const kmoe_desc& d, int Q, const float* part, const uint16_t* xb, const int8_t* w13,
+                       const float* s13, uint16_t* hb, int32_t* tidx, float* tw, const DispatchOut& o,
+                       hipStream_t st) {
+  const int E = (int)d.num_experts;
+  if (E <= 64)
+    routed_launch<1, CH>(d, Q, part, xb, w13, s13, hb, tidx, tw, o, st);
+  else if (E <= 128)
+    routed_launch<2, CH>(d, Q, part, xb, w13, s13, hb, tidx, tw, o, st);
+  else if (E <= 256)
+    routed_launch<4, CH>(d, Q, part, xb, w13, s13, hb, tidx, tw, o, st);
+  else if (E <= 512)
+    routed_launch<8, CH>(d, Q, part, xb, w13, s13, hb, tidx, tw, o, st);
+  else
+    routed_launch<16, CH>(d, Q, part, xb, w13, s13, hb, tidx, tw, o, st);
+}
+
+hipError_t launch_gateup_routed(const kmoe_desc& d, int chain, const float* part, const void* x,
+                                const kmoe_packed_experts& p, void* h_sorted, int32_t* topk_idx, float* topk_w,
+                                const DispatchOut& dout, hipStream_t st) {
+  if (!gateup_routed_fits(d)) return hipErrorInvalidValue;
+  const int Q = route_split_groups(d);
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(x);
+  const int8_t* w13 = reinterpret_cast<const int8_t*>(p.w13);
+  const float* s13 = reinterpret_cast<const float*>(p.s13);
+  uint16_t* hb = reinterpret_cast<uint16_t*>(h_sorted);
+  if (chain == kChainF32)
+    routed_epl<kChainF32>(d, Q, part, xb, w13, s13, hb, topk_idx, topk_w, dout, st);
+  else
+    routed_epl<kChainAct>(d, Q, part, xb, w13, s13, hb, topk_idx, topk_w, dout, st);
   return hipGetLastError();
 }
 

@@ -42,6 +42,13 @@ size_t route_split_part_floats(const kmoe_desc& d);
 hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part, float* logits,
                               int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm = nullptr,
                               const DispatchOut* dispatch = nullptr);
+// The split router's first kernel alone (group partials into part; with a
+// SliceNorm it also writes the normalised rows), for a caller that finishes
+// the tokens itself (launch_gateup_routed); route_split_groups(d) partials per
+// token and expert.
+hipError_t launch_route_slices(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part,
+                               hipStream_t st, const SliceNorm* norm = nullptr);
+int route_split_groups(const kmoe_desc& d);
 hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const int32_t* hist, int32_t* group_sizes,
                            int32_t* offsets, int32_t* active, int32_t* sorted_token, int32_t* sorted_expert,
                            int32_t* inv, hipStream_t st);
@@ -80,6 +87,14 @@ hipError_t launch_down_combine(const kmoe_desc& d, int chain, bool scatter, cons
                                const int32_t* topk_idx, const int32_t* inv, const float* topk_w,
                                const kmoe_packed_experts& p, void* out, hipStream_t st, const void* res);
 hipError_t launch_topk_w_cast(const kmoe_desc& d, const float* topk_w, void* out, hipStream_t st);
+// Packed decode with T <= 4 (gateup_routed_fits): the gate/up kernel finishes
+// the tokens from the split router's partials (launch_route_slices) and runs
+// the dispatch sort itself, writing topk_idx, topk_w and the dispatch arrays
+// as launch_route_split + launch_dispatch would; h_sorted is bit-identical.
+bool gateup_routed_fits(const kmoe_desc& d);
+hipError_t launch_gateup_routed(const kmoe_desc& d, int chain, const float* part, const void* x,
+                                const kmoe_packed_experts& p, void* h_sorted, int32_t* topk_idx, float* topk_w,
+                                const DispatchOut& dout, hipStream_t st);
 
 // block.hip
 size_t rms_norm_lds_bytes(int64_t D);
