@@ -302,6 +302,12 @@ def test_235b_layer(dev):
     layer = make_layer("235b", seed=1)
     cfg = layer_cfg(layer, "ragged")
     _prefill_sampled(layer, 16, seed=16, n_tok=16)
+    # 16 < T <= 64 at D = 4096: the gate/up kernel's 16-row groups spread over
+    # blocks, a skewed router putting more than 16 rows on its hot experts
+    x40 = make_x(40, layer.D, seed=40)
+    x40[:, 0] = 1.0
+    od = _prefill_sampled(layer, 40, seed=40, n_tok=16, router=skew_router(layer.router, lam=1.5), x=x40)
+    assert int(np.max(od["group_sizes"])) > 16
     _prefill_sampled(layer, 100, seed=100, n_tok=16)  # the row-group kernels
     _prefill_sampled(layer, 2048, seed=2048, n_tok=24)
     # the block call at T = 100: the split router normalising 4096-wide rows
