@@ -34,17 +34,22 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
 }
 
-// 16 int8 -> bf16(q * s) (s already rounded to bf16), one packed pair at a time
+// 16 int8 -> bf16(q * s) (s already rounded to bf16), one packed pair at a time.
+// Each byte is biased to u = q + 128 (one XOR per four bytes) and converted by
+// v_cvt_f32_ubyteN; fma(u, s, -128 s) is then q * s exactly (both terms are
+// exact and q * s has at most 16 significant bits), so the only rounding is the
+// bf16 conversion: two instructions and a half per weight.
 __device__ __forceinline__ void dequant16(const uint4 q, const float s, bf16x8& lo, bf16x8& hi) {
-  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+  const float nb = -128.0f * s;
   uint32_t o[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t v = w[j >> 1];
     const int sh = 16 * (j & 1);
-    const float a = (float)(int8_t)((v >> sh) & 0xffu);
-    const float b = (float)(int8_t)((v >> (sh + 8)) & 0xffu);
-    o[j] = pack_bf16x2(a * s, b * s);
+    const float a = (float)((v >> sh) & 0xffu);
+    const float b = (float)((v >> (sh + 8)) & 0xffu);
+    o[j] = pack_bf16x2(__builtin_fmaf(a, s, nb), __builtin_fmaf(b, s, nb));
   }
   lo = __builtin_bit_cast(bf16x8, uint4{o[0], o[1], o[2], o[3]});
   hi = __builtin_bit_cast(bf16x8, uint4{o[4], o[5], o[6], o[7]});
