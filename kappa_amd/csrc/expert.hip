@@ -813,13 +813,27 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_void*)p; }
 
 // 16 bytes per lane from global memory (sbase + voff) into LDS at lds + 16 * lane.
-// sbase and lds must be wave-uniform.
+// sbase and lds must be wave-uniform. The LDS address goes through M0: the
+// asm keeps the caller's M0 (saved and restored, so no clobber of a register
+// the compiler reserves) and puts one wait state between the SALU write of M0
+// and the LDS-DMA load that reads it (a gfx9 hazard the compiler does not see
+// inside inline asm).
 __device__ __forceinline__ void dma16(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+  uint32_t m0save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(m0save)
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory");
 }
 // The same with the nontemporal hint, for weights no other tile re-reads.
 __device__ __forceinline__ void dma16_stream(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+  uint32_t m0save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt\n\ts_mov_b32 m0, %0"
+      : "=&s"(m0save)
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory");
 }
 
 // Wait until at most N of this wave's vector-memory loads are outstanding and
