@@ -170,13 +170,14 @@ __device__ __forceinline__ int tile_expert(const int* mtp, int E, int v) {
 // int8 stays in registers across 16-row blocks. GUARD handles a chunk count
 // per wave that NB does not divide.
 //
-// DENSE (T <= 16, one batch per wave): the 16-row tile is the T tokens
-// themselves, in token order, instead of the expert's gathered rows; it pays
-// while T is small, since every block reads all T activation rows. A row's
-// products do not depend on the other rows of the tile, so each stored row is
-// the value the gathered tile gives; only the rows of the tokens routed to
-// the expert are stored. The activation loads then depend on nothing and are
-// issued first, ahead of the expert lookup.
+// DENSE (T <= 16): the 16-row tile is the T tokens themselves, in token
+// order, instead of the expert's gathered rows; it pays while T is small,
+// since every block reads all T activation rows. A row's products do not
+// depend on the other rows of the tile, so each stored row is the value the
+// gathered tile gives; only the rows of the tokens routed to the expert are
+// stored. The first load batch's activation fragments depend on nothing and
+// are issued first, ahead of the expert lookup; later batches load theirs in
+// the loop.
 // ---------------------------------------------------------------------------
 template <int WPB, int NB, bool GUARD, int MRB, bool DENSE, bool ALLROWS, int CH>
 __device__ __forceinline__ void gateup_decode_body(int ig, int slot, int rg, int T, int D, int I, int E,
@@ -186,7 +187,7 @@ __device__ __forceinline__ void gateup_decode_body(int ig, int slot, int rg, int
                                                    const int32_t* __restrict__ sorted_token,
                                                    const int8_t* __restrict__ w13, const float* __restrict__ s13,
                                                    uint16_t* __restrict__ h_sorted, int cap) {
-  static_assert(!DENSE || (MRB == 1 && !GUARD), "dense tiles: one row block, one batch per wave");
+  static_assert(!DENSE || (MRB == 1 && !GUARD), "dense tiles: one row block, whole load batches");
   static_assert(!ALLROWS || (!DENSE && !GUARD), "row groups: gathered rows, one batch per wave");
   static_assert(WPB == 8 || WPB == 4, "eight reduction parts over eight or four waves");
   constexpr int PPW = 8 / WPB;  // reduction parts per wave
@@ -289,8 +290,20 @@ __device__ __forceinline__ void gateup_decode_body(int ig, int slot, int rg, int
 #pragma unroll
           for (int i = 0; i < NB; ++i) {
             if (DENSE) {
-              a0[i] = da0[i];
-              a1[i] = da1[i];
+              if (cb == c0) {
+                a0[i] = da0[i];
+                a1[i] = da1[i];
+              } else {
+                // a later batch: the T token rows at its chunks
+                const int t = lane & 15;
+                a0[i] = uint4{0, 0, 0, 0};
+                a1[i] = uint4{0, 0, 0, 0};
+                if (t < T) {
+                  const uint4* ap = reinterpret_cast<const uint4*>(x + (size_t)t * D + koff + (cb + i) * 64);
+                  a0[i] = ap[0];
+                  a1[i] = ap[1];
+                }
+              }
               continue;
             }
             a0[i] = uint4{0, 0, 0, 0};
@@ -1449,23 +1462,19 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
     // the reduction, batches of 4 (gate/up) or 3 (down) chunks per load stage
     if (stages & kStageGateUp) {
       if (T <= 16 && (D / 64 == 32 || D / 64 == 64)) {
-        // at most one 16-row block per expert: eight waves of one load batch
-        // each (4 chunks at D = 2048, 8 at D = 4096), every load of a wave in
-        // flight at once. Up to T = 4 the tile is the T tokens themselves
-        // (DENSE); beyond, gathering only the expert's rows reads less.
+        // at most one 16-row block per expert: eight waves of load batches of
+        // four chunks (one batch at D = 2048, two at D = 4096). Up to T = 4 the
+        // tile is the T tokens themselves (DENSE); beyond, gathering only the
+        // expert's rows reads less. At D = 4096 one batch of eight chunks (170
+        // VGPRs, one block per CU) left 235B-A22B decode T=16 at 306 us; two
+        // batches of four keep two blocks per CU: 258 us.
         const dim3 grid(I / 16, slots);
         const bool dense = T <= 4;
-        if (D / 64 == 32 && dense)
+        if (dense)
           hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, true, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
                              xb, offsets, active, sorted_token, w13, s13, hb, cap);
-        else if (D / 64 == 32)
-          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, false, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
-                             xb, offsets, active, sorted_token, w13, s13, hb, cap);
-        else if (dense)
-          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, true, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
-                             xb, offsets, active, sorted_token, w13, s13, hb, cap);
         else
-          hipLaunchKernelGGL((k_gateup_decode<8, 8, false, 1, false, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
+          hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, false, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
                              xb, offsets, active, sorted_token, w13, s13, hb, cap);
       } else {
         // one 16-row block per block, the expert's rows spread over grid z
@@ -1765,14 +1774,10 @@ static void routed_launch(const kmoe_desc& d, int Q, const float* part, const ui
   // at most min(T*K, E) active experts; two blocks per CU are resident
   const int items = (I / 16) * std::min(T * K, E);
   const dim3 grid(std::min(items, 2 * cu_count()));
-  if (D == 32 * 64)
-    hipLaunchKernelGGL((k_gateup_routed<EPL, 4, CH>), grid, dim3(512), 0, st, T, D, I, E, K, Q, part, 1, xb, w13, s13,
-                       hb, capacity_of(d), tidx, tw, o.group_sizes, o.offsets, o.active, o.sorted_token,
-                       o.sorted_expert, o.inv);
-  else
-    hipLaunchKernelGGL((k_gateup_routed<EPL, 8, CH>), grid, dim3(512), 0, st, T, D, I, E, K, Q, part, 1, xb, w13, s13,
-                       hb, capacity_of(d), tidx, tw, o.group_sizes, o.offsets, o.active, o.sorted_token,
-                       o.sorted_expert, o.inv);
+  // load batches of four chunks at both hidden sizes (two per wave at D = 4096)
+  hipLaunchKernelGGL((k_gateup_routed<EPL, 4, CH>), grid, dim3(512), 0, st, T, D, I, E, K, Q, part, 1, xb, w13, s13,
+                     hb, capacity_of(d), tidx, tw, o.group_sizes, o.offsets, o.active, o.sorted_token,
+                     o.sorted_expert, o.inv);
 }
 
 template <int CH>

@@ -316,9 +316,11 @@ def test_235b_layer(dev):
     sc = (1.0 + 0.1 * torch.randn(layer.D, device=dev)).to(torch.bfloat16)
     composed = h + moe_swiglu_ffn(rms_norm(h, sc), layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
     assert torch.equal(moe_block_ffn(h, sc, layer.router, layer.gate, layer.up, layer.down, cfg=cfg), composed)
-    # T = 1 and 2: the whole layer (fused down + combine, each wave holding 12 of
-    # the 24 chunks of the reduction) against the staged calls
-    for T in (1, 2):
+    # T = 1, 2 and 4: the whole layer (the gate/up kernel finishing the routing
+    # itself, its dense token tile in two load batches per wave; fused down +
+    # combine, each wave holding 12 of the 24 chunks of the reduction) against
+    # the staged calls
+    for T in (1, 2, 4):
         _prefill_sampled(layer, T, seed=T, n_tok=T)
         x = make_x(T, layer.D, seed=T)
         r, d = _route_and_dispatch(x, layer.router, layer.E, layer.K)
@@ -326,6 +328,14 @@ def test_235b_layer(dev):
         staged = moe_stages.combine(y, d["inv"], r["w"], k=layer.K, impl="ragged")
         out = moe_swiglu_ffn(x.reshape(1, T, layer.D), layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
         assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
+    # a token's output does not depend on its batch across the D = 4096 shape
+    # switches: dense tile / gathered rows (T = 4/5), eight / four gate/up waves
+    # (T = 16/17)
+    for T in (4, 16):
+        x = make_x(T + 1, layer.D, seed=900 + T)
+        a = moe_swiglu_ffn(x[:T].reshape(1, T, layer.D), layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
+        b = moe_swiglu_ffn(x.reshape(1, T + 1, layer.D), layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
+        assert torch.equal(a.reshape(T, layer.D), b.reshape(T + 1, layer.D)[:T]), f"T={T}"
     del layer
     torch.cuda.empty_cache()
 
