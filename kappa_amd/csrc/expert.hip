@@ -1461,16 +1461,14 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
     // shapes from a sweep on MI355X (30B-A3B layer, T = 1..64): four waves split
     // the reduction, batches of 4 (gate/up) or 3 (down) chunks per load stage
     if (stages & kStageGateUp) {
-      if (T <= 16 && (D / 64 == 32 || D / 64 == 64)) {
-        // at most one 16-row block per expert: eight waves of load batches of
-        // four chunks (one batch at D = 2048, two at D = 4096). Up to T = 4 the
-        // tile is the T tokens themselves (DENSE); beyond, gathering only the
-        // expert's rows reads less. At D = 4096 one batch of eight chunks (170
-        // VGPRs, one block per CU) left 235B-A22B decode T=16 at 306 us; two
-        // batches of four keep two blocks per CU: 258 us.
+      if ((T <= 4 && D / 64 == 32) || (T <= 16 && D / 64 == 64)) {
+        // eight waves of load batches of four chunks (one batch at D = 2048,
+        // two at D = 4096), at most one 16-row block per expert; up to four
+        // tokens the tile is the T tokens themselves (DENSE), beyond it the
+        // expert's gathered rows. At D = 4096 this beats the four-wave form
+        // below up to 16 tokens (235B-A22B T=16 241 against 258 us per layer).
         const dim3 grid(I / 16, slots);
-        const bool dense = T <= 4;
-        if (dense)
+        if (T <= 4)
           hipLaunchKernelGGL((k_gateup_decode<8, 4, false, 1, true, false, CH>), grid, dim3(512), 0, st, T, D, I, E,
                              xb, offsets, active, sorted_token, w13, s13, hb, cap);
         else
@@ -1481,7 +1479,9 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
         // (ceil(T/16) groups; an expert has at most T rows); four waves of two
         // reduction parts each. Against one block holding all of an expert's
         // rows (up to four 16-row blocks): decode T=64 gate/up 70 -> 64 us,
-        // from the smaller register and LDS footprint.
+        // from the smaller register and LDS footprint. At D = 2048 it also
+        // beats the eight-wave form from five tokens on (30B-A3B T=16 gate/up
+        // 45.4 -> 42.9 us, T=8 29.8 -> 28.9 us).
         const dim3 grid(I / 16, slots, (T + 15) / 16);
         if ((D / 64) % 16 == 0)
           hipLaunchKernelGGL((k_gateup_decode<4, 4, false, 1, false, false, CH>), grid, dim3(256), 0, st, T, D, I, E,
