@@ -84,10 +84,10 @@ __device__ __forceinline__ float load_scale(const void* scale, int scale_bf16, i
 // G wave-groups one after the other; the tree levels st < SPW are shuffles
 // between lane groups, the levels SPW <= st < SPW*G combine the G wave-groups
 // in registers, and the remaining levels combine the waves' partials through
-// LDS. x for the TB tokens of the block is staged in LDS as f32
-// [slice][64][TB] (slice pitch padded by 4 floats: the lane groups of a wave
-// read different slices in distinct banks); the same LDS then holds the wave
-// partials [wave][TB][E].
+// LDS, one element's partials per thread. x for the TB tokens of the block
+// is staged in LDS as f32 [slice][64][TB] (slice pitch padded by 4 floats:
+// the lane groups of a wave read different slices in distinct banks); the
+// same LDS then holds the wave partials [wave][TB][E].
 //
 // Then one wave per token selects the top K (value descending, ties to the
 // lower expert index; NaN ranks as -inf) with K wave-wide arg-max rounds, and
@@ -239,15 +239,21 @@ __global__ __launch_bounds__(1024) void k_route(int T, int D, int E, int K, int 
         if (e0 + i < E) part[(size_t)w * TE + tt * E + e0 + i] = p0.v[tt][i];
   }
   __syncthreads();
-  // the tree levels across waves, in place: part[g] += part[g + st]
-  for (int st = 1; st < NWB; st <<= 1) {
-    const int n = (NWB / (2 * st)) * TE;
-    for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
-      const int g = (idx / TE) * 2 * st, rem = idx - (idx / TE) * TE;
-      part[(size_t)g * TE + rem] = part[(size_t)g * TE + rem] + part[(size_t)(g + st) * TE + rem];
-    }
-    __syncthreads();
+  // the tree levels across the NWB waves (a power of two, at most 16): a
+  // thread takes an element's NWB partials and applies the levels
+  // p[g] += p[g + st], st = 1, 2, 4, 8, in registers
+  for (int rem = threadIdx.x; rem < TE; rem += blockDim.x) {
+    float v[16];
+#pragma unroll
+    for (int g = 0; g < 16; ++g) v[g] = g < NWB ? part[(size_t)g * TE + rem] : 0.0f;
+#pragma unroll
+    for (int st = 1; st < 16; st <<= 1)
+#pragma unroll
+      for (int g = 0; g + st < 16; g += 2 * st)
+        if (g + st < NWB) v[g] = v[g] + v[g + st];
+    part[rem] = v[0];
   }
+  __syncthreads();
 
   // top-k: lane owns experts lane + 64*i, i < EPL (E <= 64 * EPL); the
   // per-wave selection scratch sits after the partials
