@@ -517,6 +517,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--quick", action="store_true", help="only the 30B decode and prefill points")
+    ap.add_argument(
+        "--only-235b",
+        action="store_true",
+        help="only the 235B-A22B layer's decode T=16 and prefill T=2048 points (for kernel traces)",
+    )
     ap.add_argument("--decode", default="1,8,32,64", help="decode token counts; the largest is the headline")
     ap.add_argument("--prefill", default="512,2048,4096", help="prefill token counts ('' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -557,6 +562,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only_235b:
+        print(json.dumps({"layer_235b": bench_235b(args, dev)}), flush=True)
+        return
     R = args.copies
     log(f"bench: building {R} weight copies of the 30B-A3B W8 layer")
     layers = [make_layer("30b", seed=i) for i in range(R)]
