@@ -1032,9 +1032,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   const int rem = L - mtp[e] * NT;
   const int nt = __builtin_amdgcn_readfirstlane(rem / nmt_e);
   const int mt = rem - nt * nmt_e;
-  const int row0 = __builtin_amdgcn_readfirstlane(offsets[e] + mt * kGemmRows);
-  const int rows =
-      __builtin_amdgcn_readfirstlane(min(kGemmRows, offsets[e] + min(offsets[e + 1] - offsets[e], cap) - row0));
+  // the expert's rows split evenly over its nmt_e row tiles (multiples of 16
+  // rows; every tile gets at least one row): tiles of one column block then run
+  // at the same pace and meet each other's weight chunks in L2, where a full
+  // tile and a nearly empty one would each fetch them
+  const int ne = min(offsets[e + 1] - offsets[e], cap);
+  const int tr = (((ne + nmt_e - 1) / nmt_e) + 15) & ~15;
+  const int row0 = __builtin_amdgcn_readfirstlane(offsets[e] + mt * tr);
+  const int rows = __builtin_amdgcn_readfirstlane(min(tr, ne - mt * tr));
   if (tid < kGemmRows) tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
   __syncthreads();
 
