@@ -391,7 +391,7 @@ kmoe_status forward_general(const kmoe_desc* desc, const void* x, const void* xi
 
 // The stage sequence of moe_swiglu_ffn on x. With a norm, x is the residual
 // stream h: the block runs on h2 = rms_norm(h) (norm->h2, computed by the
-// split router at T <= 128, else by the norm kernel) and the combine adds the
+// split router at T <= 240, else by the norm kernel) and the combine adds the
 // block's rounded output to h.
 kmoe_status forward_stages(const kmoe_desc* desc, const void* x, const kmoe_host::SliceNorm* norm,
                            const kmoe_weight* router, const kmoe_weight* gate, const kmoe_weight* up,

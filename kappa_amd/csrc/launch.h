@@ -12,8 +12,11 @@ hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& ro
                         float* topk_w, int32_t* hist, hipStream_t st);
 // per-64-token-chunk expert histograms of the selections (for launch_dispatch)
 hipError_t launch_dispatch_count(const kmoe_desc& d, const int32_t* topk_idx, int32_t* hist, hipStream_t st);
-// The whole-block call routes up to this many tokens with the split router.
-constexpr int kSplitRouterMaxTokens = 128;
+// The whole-block call routes up to this many tokens with the split router
+// (at T=256 the split router took 13 us against 21 us for k_route, whose
+// blocks then hold one token each; from 512 tokens on they are even; 240 keeps
+// every call up to 272 tokens inside the no-allocation scratch).
+constexpr int kSplitRouterMaxTokens = 240;
 // Split router (many blocks per token; same logits and selections as
 // launch_route): part holds route_split_part_floats(d) floats of workspace.
 // With a SliceNorm, x is the residual stream h: the router reduces and
