@@ -795,9 +795,9 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
 // ---------------------------------------------------------------------------
 // Prefill grouped GEMM over (expert, row tile, column tile) work items.
 //
-// A block of four waves computes up to 128 rows x 256 B columns (gate/up: 128
-// gate + 128 up columns, i.e. 128 columns of h; down: 256 output columns);
-// two blocks share a CU. Wave w owns the 16-column cells 4w .. 4w+3 (gate/up:
+// A block of four waves computes up to 128 (or 160) rows x 256 B columns
+// (gate/up: 128 gate + 128 up columns, i.e. 128 columns of h; down: 256 output
+// columns); two blocks share a CU. Wave w owns the 16-column cells 4w .. 4w+3 (gate/up:
 // two gate cells and the matching two up cells, so the SwiGLU epilogue pairs
 // registers of one lane) for all rows, in accumulator tiles of
 // v_mfma_f32_16x16x32_bf16, and dequantises its cells to bf16(q * bf16(s)) in
@@ -809,15 +809,17 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
 // cells, whose 16 bytes per lane are exactly one lane's MFMA fragment of one
 // column) in a 3-stage ring, so the weights, which come from HBM, are
 // requested two chunks ahead and the activation rows, mostly L2 hits, one
-// chunk ahead. 80 KB per block: two blocks fill the CU's LDS. The loads are
+// chunk ahead. 80 KB per block: two blocks fill the CU's LDS. The 160-row form
+// (for experts with 96 rows or more on average) has a 20 KB A stage and a
+// 2-stage weight ring (72 KB): the gate/up weights then come one chunk ahead,
+// the down weights (read for two chunks of h planes) still two. The loads are
 // inline asm, so the compiler's wait-count pass does not see them: every wave
 // issues the same loads in the same order and the chunk loop waits for them
 // itself (vmcnt is in-order), then a barrier publishes the stage and frees
 // the ones read last.
 //
 // Rows past the expert's end are loaded from a clamped copy of row 0 and never
-// stored; the loop body is instantiated for 8, 4, 2 and 1 active 16-row
-// tiles. Work items are ordered (expert, column tile, row tile) and
+// stored; the loop body is instantiated for 1 to 8 (10) active 16-row tiles. Work items are ordered (expert, column tile, row tile) and
 // consecutive items go to the same XCD, so the row tiles of one expert share
 // its weights, and the column tiles its rows, in that XCD's L2.
 // ---------------------------------------------------------------------------
@@ -865,16 +867,28 @@ __device__ __forceinline__ void vm_barrier() {
 __device__ __forceinline__ int a_piece(int r, int p) { return p ^ (r & 7); }
 __device__ __forceinline__ int a_swz(int r, int p) { return r * 64 + (a_piece(r, p) << 3); }
 
-constexpr int kGemmRows = 128;                // rows per tile
-constexpr int kGemmA = kGemmRows * 128;       // A stage: 128 rows x 64 bf16 (16 KB)
+constexpr int kGemmRows = 128;                // rows per tile (the 128-row form)
 constexpr int kGemmB = 16 * 1024;             // B stage: 16 cells x 64 k x 16 columns int8
-constexpr int kGemmNA = 2, kGemmNB = 3;       // ring depths
-constexpr int kGemmLds = kGemmNA * kGemmA + kGemmNB * kGemmB;  // 80 KB: two blocks fill the CU's LDS
-constexpr int kGemmAJ = 4, kGemmBJ = 4;       // loads per wave per chunk (A: 8 rows each, B: one cell)
+constexpr int kGemmBJ = 4;                    // B loads per wave per chunk (one cell each)
+
+// Tile shapes: 128 rows with a weight ring three chunks deep (80 KB), or 160
+// rows with a ring two chunks deep (72 KB; an expert with up to 160 rows is
+// one tile). Either way two blocks fill a CU's LDS.
+template <int RW>
+struct GemmShape {
+  static_assert(RW == 128 || RW == 160, "tile rows");
+  static constexpr int kRows = RW;
+  static constexpr int kA = RW * 128;          // A stage: RW rows x 64 bf16
+  static constexpr int kAJ = RW / 32;          // A loads per wave per chunk (8 rows each)
+  static constexpr int kNA = 2;                // A ring depth
+  static constexpr int kNB = RW == 128 ? 3 : 2;  // B ring depth
+  static constexpr int kLds = kNA * kA + kNB * kGemmB;
+};
 
 // Per-wave load descriptors of one tile.
+template <int AJ>
 struct GemmLoads {
-  uint32_t avoff[kGemmAJ];  // byte offsets (per lane) of this wave's A loads in src
+  uint32_t avoff[AJ];       // byte offsets (per lane) of this wave's A loads in src
   const int8_t* bsrc[4];    // this wave's four B cells, at chunk 0
   float sc[4];              // their scales (column lane % 16)
 };
@@ -884,10 +898,12 @@ struct GemmLoads {
 // its lo plane (2 * KCW chunks); A chunk c is plane c & 1 of weight chunk
 // c >> 1, so each weight chunk is loaded and converted once and meets both
 // planes in two consecutive iterations.
-template <bool GATEUP, int MT, bool NTB, int CH, int PL>
-__device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, int KCW, int wv, int rows, int row0,
-                                          int nt, const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
-                                          int Ndim) {
+template <bool GATEUP, int MT, bool NTB, int CH, int PL, int RW>
+__device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads<GemmShape<RW>::kAJ>& gl, int KCW, int wv,
+                                          int rows, int row0, int nt, const uint16_t* __restrict__ src,
+                                          uint16_t* __restrict__ dst, int Ndim) {
+  using Sh = GemmShape<RW>;
+  constexpr int kGemmA = Sh::kA, kGemmAJ = Sh::kAJ, kGemmNA = Sh::kNA, kGemmNB = Sh::kNB;
   const int lane = threadIdx.x & 63;
   const uint32_t lds0 = lds_addr(smem);
   const uint8_t* const bring = smem + kGemmNA * kGemmA;
@@ -915,15 +931,19 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
     }
   };
 
-  // PL = 1. Issue order: B(0), A(0), B(1); then iteration c issues A(c+1),
-  // B(c+2) and at its end waits for A(c+1) and B(c+1) (only B(c+2) may be
-  // outstanding).
-  // PL = 2. Issue order: B(0), A(0); iteration c issues A(c+1) and, when c is
-  // even, B(c/2 + 1); at its end it waits for A(c+1) (c even: B(c/2 + 1) may
-  // stay outstanding) or for everything (c odd: B((c+1)/2) is read next).
+  // PL = 1, three B stages. Issue order: B(0), A(0), B(1); then iteration c
+  // issues A(c+1), B(c+2) and at its end waits for A(c+1) and B(c+1) (only
+  // B(c+2) may be outstanding).
+  // PL = 1, two B stages: B(0), A(0); iteration c issues A(c+1) and B(c+1)
+  // (into the stage B(c-1) left) and at its end waits for both.
+  // PL = 2 (two stages suffice). Issue order: B(0), A(0); iteration c issues
+  // A(c+1) and, when c is even, B(c/2 + 1); at its end it waits for A(c+1)
+  // (c even: B(c/2 + 1) may stay outstanding) or for everything (c odd:
+  // B((c+1)/2) is read next).
+  constexpr int kAhead = PL == 1 && kGemmNB == 3 ? 2 : 1;  // weight chunks issued ahead (PL = 1)
   issue_b(0);
   issue_a(0);
-  if (PL == 1 && 1 < KC) {
+  if (PL == 1 && kAhead == 2 && 1 < KC) {
     issue_b(1);
     vm_barrier<kGemmBJ>();
   } else {
@@ -934,9 +954,9 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
     const int b = PL == 2 ? c >> 1 : c;
     bool b_ahead = false;  // a weight chunk issued this iteration
     if (c + 1 < KC) issue_a(c + 1);
-    if (PL == 1 && c + 2 < KC) {
-      issue_b(c + 2);
-      b_ahead = true;
+    if (PL == 1 && c + kAhead < KC) {
+      issue_b(c + kAhead);
+      b_ahead = kAhead == 2;
     }
     if (PL == 2 && (c & 1) == 0 && b + 1 < KCW) {
       issue_b(b + 1);
@@ -1006,20 +1026,21 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads& gl, in
 // y_sorted. src must span fewer than 2^32 bytes (32-bit load offsets).
 // NTB: the weights are loaded with the nontemporal hint (few rows per expert,
 // so no second row tile would find them in L2).
-template <bool GATEUP, bool NTB, int CH>
+template <bool GATEUP, bool NTB, int CH, int RW>
 __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint16_t* __restrict__ src,
                                                   const int32_t* __restrict__ offsets,
                                                   const int32_t* __restrict__ sorted_token,
                                                   const int8_t* __restrict__ wp, const float* __restrict__ sp,
                                                   uint16_t* __restrict__ dst, int cap) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kGemmLds];
+  using Sh = GemmShape<RW>;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[Sh::kLds];
   // set-up scratch inside the ring (no loads are in flight yet)
   int* const mtp = reinterpret_cast<int*>(smem);
   int* const tok = mtp + kMaxExperts + 1;
-  int* const wsum = tok + kGemmRows;
+  int* const wsum = tok + RW;
   const int tid = threadIdx.x, lane = tid & 63;
   const int NT = GATEUP ? I / 128 : D / 256;
-  tile_prefix<kGemmRows>(offsets, E, cap, mtp, wsum);
+  tile_prefix<RW>(offsets, E, cap, mtp, wsum);
   const int ntiles = mtp[E] * NT;
   const int per = (ntiles + 7) >> 3;
   const int q = blockIdx.x >> 3;
@@ -1040,7 +1061,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   const int tr = (((ne + nmt_e - 1) / nmt_e) + 15) & ~15;
   const int row0 = __builtin_amdgcn_readfirstlane(offsets[e] + mt * tr);
   const int rows = __builtin_amdgcn_readfirstlane(min(tr, ne - mt * tr));
-  if (tid < kGemmRows) tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
+  if (tid < RW) tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
   __syncthreads();
 
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1048,11 +1069,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   const int Kdim = GATEUP ? D : (CH == kChainF32 ? 2 * I : I);
   const int KCW = (GATEUP ? D : I) >> 6;
   const int Ndim = GATEUP ? I : D;
-  GemmLoads gl;
-  // A load j of wave wv covers tile rows 8q .. 8q+7, q = wv * 4 + j: lane -> (row, LDS piece lane % 8)
+  GemmLoads<Sh::kAJ> gl;
+  // A load j of wave wv covers tile rows 8q .. 8q+7, q = wv * AJ + j: lane -> (row, LDS piece lane % 8)
 #pragma unroll
-  for (int j = 0; j < kGemmAJ; ++j) {
-    const int r = 8 * (wv * kGemmAJ + j) + (lane >> 3);
+  for (int j = 0; j < Sh::kAJ; ++j) {
+    const int r = 8 * (wv * Sh::kAJ + j) + (lane >> 3);
     const int t = tok[r] >= 0 ? tok[r] : tok[0];
     gl.avoff[j] = ((uint32_t)t * (uint32_t)Kdim + (uint32_t)(a_piece(r, lane & 7) << 3)) * 2u;
   }
@@ -1075,32 +1096,37 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   asm volatile("" ::"v"(gl.sc[0]), "v"(gl.sc[1]), "v"(gl.sc[2]), "v"(gl.sc[3]));
   __syncthreads();
   constexpr int PL = !GATEUP && CH == kChainF32 ? 2 : 1;  // h planes of the down product
-  // as many 16-row MFMA tiles as the rows need (an expert's last row tile is
-  // usually partial)
+  // as many 16-row MFMA tiles as the rows need
   switch ((rows + 15) >> 4) {
+    case 10:
+      if constexpr (RW >= 160) gemm_tile<GATEUP, 10, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
+    case 9:
+      if constexpr (RW >= 144) gemm_tile<GATEUP, 9, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      break;
     case 8:
-      gemm_tile<GATEUP, 8, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      gemm_tile<GATEUP, 8, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 7:
-      gemm_tile<GATEUP, 7, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      gemm_tile<GATEUP, 7, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 6:
-      gemm_tile<GATEUP, 6, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      gemm_tile<GATEUP, 6, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 5:
-      gemm_tile<GATEUP, 5, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      gemm_tile<GATEUP, 5, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 4:
-      gemm_tile<GATEUP, 4, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      gemm_tile<GATEUP, 4, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 3:
-      gemm_tile<GATEUP, 3, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      gemm_tile<GATEUP, 3, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 2:
-      gemm_tile<GATEUP, 2, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      gemm_tile<GATEUP, 2, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     default:
-      gemm_tile<GATEUP, 1, NTB, CH, PL>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      gemm_tile<GATEUP, 1, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
   }
 }
@@ -1544,29 +1570,42 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
   const uint64_t hrow = CH == kChainF32 ? 2ull * I : (uint64_t)I;
   const bool small_src = (uint64_t)T * D * 2 < (1ull << 32) && (uint64_t)M * hrow * 2 < (1ull << 32);
   if (I % 128 == 0 && D % 256 == 0 && small_src) {
-    const int upper_mt = (M + kGemmRows - 1) / kGemmRows + slots;
-    auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };
     // weights that only one row tile per expert reads (up to 64 rows per
     // expert on average) stream past the caches: T = 256 / 512 / 1024 gain
     // 14 / 9 / 6 us per layer; at 128 rows per expert (T = 2048) the second
     // tiles of the busier experts lose their L2 hits (+8 us)
     const bool ntb = M <= E * kGemmRows / 2;
+    // 160-row tiles from 96 rows per expert on average: an expert's rows take
+    // fewer tiles, each converting the same weight chunks (T = 1536 / 2048 /
+    // 4096: 308 -> 294, 339 -> 328, 550 -> 509 us per layer; 235B-A22B at
+    // T = 2048 1051 -> 937 us); below that the three-deep weight ring of the
+    // 128-row form hides more of the weight stream's latency
+    const bool big = M >= E * 96;
+    const int rw = big ? 160 : kGemmRows;
+    const int upper_mt = (M + rw - 1) / rw + slots;
+    auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };
     if (stages & kStageGateUp) {
       if (ntb)
-        hipLaunchKernelGGL((k_gemm<true, true, CH>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb, offsets,
-                           sorted_token, w13, s13, hb, cap);
+        hipLaunchKernelGGL((k_gemm<true, true, CH, 128>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
+                           offsets, sorted_token, w13, s13, hb, cap);
+      else if (big)
+        hipLaunchKernelGGL((k_gemm<true, false, CH, 160>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
+                           offsets, sorted_token, w13, s13, hb, cap);
       else
-        hipLaunchKernelGGL((k_gemm<true, false, CH>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
+        hipLaunchKernelGGL((k_gemm<true, false, CH, 128>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
                            offsets, sorted_token, w13, s13, hb, cap);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
     }
     if (stages & kStageDown) {
       if (ntb)
-        hipLaunchKernelGGL((k_gemm<false, true, CH>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb, offsets,
-                           sorted_token, w2, s2, yb, cap);
+        hipLaunchKernelGGL((k_gemm<false, true, CH, 128>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
+                           offsets, sorted_token, w2, s2, yb, cap);
+      else if (big)
+        hipLaunchKernelGGL((k_gemm<false, false, CH, 160>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
+                           offsets, sorted_token, w2, s2, yb, cap);
       else
-        hipLaunchKernelGGL((k_gemm<false, false, CH>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
+        hipLaunchKernelGGL((k_gemm<false, false, CH, 128>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
                            offsets, sorted_token, w2, s2, yb, cap);
       return hipGetLastError();
     }
