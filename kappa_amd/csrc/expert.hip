@@ -1581,12 +1581,18 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
     // T = 2048 1051 -> 937 us); below that the three-deep weight ring of the
     // 128-row form hides more of the weight stream's latency
     const bool big = M >= E * 96;
+    // with up to 128 rows per expert on average a 160-row tile is mostly the
+    // expert's only one: its weights stream past the caches as well
+    const bool ntb160 = big && M <= E * 128;
     const int rw = big ? 160 : kGemmRows;
     const int upper_mt = (M + rw - 1) / rw + slots;
     auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };
     if (stages & kStageGateUp) {
       if (ntb)
         hipLaunchKernelGGL((k_gemm<true, true, CH, 128>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
+                           offsets, sorted_token, w13, s13, hb, cap);
+      else if (ntb160)
+        hipLaunchKernelGGL((k_gemm<true, true, CH, 160>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
                            offsets, sorted_token, w13, s13, hb, cap);
       else if (big)
         hipLaunchKernelGGL((k_gemm<true, false, CH, 160>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
@@ -1600,6 +1606,9 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
     if (stages & kStageDown) {
       if (ntb)
         hipLaunchKernelGGL((k_gemm<false, true, CH, 128>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
+                           offsets, sorted_token, w2, s2, yb, cap);
+      else if (ntb160)
+        hipLaunchKernelGGL((k_gemm<false, true, CH, 160>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
                            offsets, sorted_token, w2, s2, yb, cap);
       else if (big)
         hipLaunchKernelGGL((k_gemm<false, false, CH, 160>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
