@@ -98,7 +98,7 @@ def _norm_scale(D, seed, dev):
     return torch.from_numpy((1.0 + 0.1 * rng.standard_normal(D)).astype(np.float32)).to(dev).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("T", [1, 2, 8, 17, 64, 65, 128, 129, 4096])
+@pytest.mark.parametrize("T", [1, 2, 8, 17, 64, 65, 128, 129, 240, 241, 4096])
 def test_30b_fused_block_equals_separate_calls(dev, l30, T):
     """moe_block_ffn == h + moe_swiglu_ffn(rms_norm(h)), bit for bit; the norm is
     checked against the oracle on every row, the MoE half against the oracle
