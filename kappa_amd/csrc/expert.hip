@@ -797,8 +797,8 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
 //
 // A block of four waves computes up to 128 (or 160) rows x 256 B columns
 // (gate/up: 128 gate + 128 up columns, i.e. 128 columns of h; down: 256 output
-// columns); two blocks share a CU. Wave w owns the 16-column cells 4w .. 4w+3 (gate/up:
-// two gate cells and the matching two up cells, so the SwiGLU epilogue pairs
+// columns); two blocks share a CU. Wave w owns the 16-column cells 4w .. 4w+3
+// (gate/up: two gate cells and the matching two up cells, so the SwiGLU epilogue pairs
 // registers of one lane) for all rows, in accumulator tiles of
 // v_mfma_f32_16x16x32_bf16, and dequantises its cells to bf16(q * bf16(s)) in
 // registers once per 64-deep k chunk.
@@ -819,8 +819,9 @@ __global__ __launch_bounds__(256, 2) void k_prefill(int D, int I, int E, const u
 // the ones read last.
 //
 // Rows past the expert's end are loaded from a clamped copy of row 0 and never
-// stored; the loop body is instantiated for 1 to 8 (10) active 16-row tiles. Work items are ordered (expert, column tile, row tile) and
-// consecutive items go to the same XCD, so the row tiles of one expert share
+// stored; the loop body is instantiated for 1 to 8 (10) active 16-row tiles.
+// Work items are ordered (expert, column tile, row tile) and consecutive items
+// go to the same XCD, so the row tiles of one expert share
 // its weights, and the column tiles its rows, in that XCD's L2.
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
@@ -1099,10 +1100,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   // as many 16-row MFMA tiles as the rows need
   switch ((rows + 15) >> 4) {
     case 10:
-      if constexpr (RW >= 160) gemm_tile<GATEUP, 10, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      if constexpr (RW >= 160)
+        gemm_tile<GATEUP, 10, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 9:
-      if constexpr (RW >= 144) gemm_tile<GATEUP, 9, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      if constexpr (RW >= 144)
+        gemm_tile<GATEUP, 9, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 8:
       gemm_tile<GATEUP, 8, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
