@@ -447,7 +447,10 @@ __global__ __launch_bounds__(512) void k_gateup_routed(int T, int D, int I, int 
   const int w = threadIdx.x >> 6;
   if (w < T) finish_token<EPL>(w, E, K, Q, part, nullptr, l_tidx, l_tw, out_bf16, sel, tk[w]);
   __syncthreads();
-  dispatch_chunk(T, E, K, 0, 1, sel, nullptr, l_gs, l_off, l_act, l_stok, l_sexp, l_inv, cap, L);
+  if (dispatch_fits_wave(T * K, E))
+    dispatch_wave(T, E, K, sel, l_gs, l_off, l_act, l_stok, l_sexp, l_inv, cap);
+  else
+    dispatch_chunk(T, E, K, 0, 1, sel, nullptr, l_gs, l_off, l_act, l_stok, l_sexp, l_inv, cap, L);
   __syncthreads();
   if (blockIdx.x == 0) {
     const int M = T * K;

@@ -461,8 +461,11 @@ __global__ __launch_bounds__(64 * NW) void k_route_finish_dispatch(
   const int w = threadIdx.x >> 6;
   if (w < T) finish_token<EPL>(w, E, K, Q, part, logits, topk_idx, topk_w, out_bf16, idx_lds, tk[w]);
   __syncthreads();
-  dispatch_chunk(T, E, K, 0, 1, idx_lds, nullptr, group_sizes, offsets, active, sorted_token, sorted_expert, inv, cap,
-                 L);
+  if (dispatch_fits_wave(T * K, E))
+    dispatch_wave(T, E, K, idx_lds, group_sizes, offsets, active, sorted_token, sorted_expert, inv, cap);
+  else
+    dispatch_chunk(T, E, K, 0, 1, idx_lds, nullptr, group_sizes, offsets, active, sorted_token, sorted_expert, inv,
+                   cap, L);
 }
 
 __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, int nblk,

@@ -309,4 +309,58 @@ static __device__ void dispatch_chunk(int T, int E, int K, int b, int nblk, cons
   }
 }
 
+// The same dispatch by one wave with no barrier, for a call with at most 8
+// assignments (one token) and 256 experts (every thread may call it; wave 0
+// works). sel holds the T*K row-major selections (LDS or global, read by all
+// lanes at once). Assignment m = lane: its position is the number of
+// assignments with a smaller expert plus the earlier ones with the same expert
+// (the stable sort); an expert's count and offset come from one pass over the
+// selections. It is correct up to 64 assignments, but its serial passes cost
+// more than dispatch_chunk's barriers from 16 assignments on (T=1 decode
+// layer 24.4 -> 23.7 us; T=4 and T=8 2 and 5 us slower).
+__device__ __forceinline__ bool dispatch_fits_wave(int M, int E) { return M <= 8 && E <= 256; }
+
+static __device__ void dispatch_wave(int T, int E, int K, const int32_t* sel, int32_t* __restrict__ group_sizes,
+                                     int32_t* __restrict__ offsets, int32_t* __restrict__ active,
+                                     int32_t* __restrict__ sorted_token, int32_t* __restrict__ sorted_expert,
+                                     int32_t* __restrict__ inv, int cap) {
+  if ((threadIdx.x >> 6) != 0) return;
+  const int lane = threadIdx.x & 63;
+  const int M = T * K;
+  const int em = lane < M ? sel[lane] : -1;
+  int below = 0, before = 0;
+  for (int i = 0; i < M; ++i) {
+    const int ei = sel[i];
+    below += ei < em;
+    before += ei == em && i < lane;
+  }
+  // an assignment that is its expert's first: its index among the active experts
+  const bool first = lane < M && before == 0;
+  const unsigned long long firsts = __ballot(first);
+  int rank = 0;
+  for (int i = 0; i < M; ++i)
+    if ((firsts >> i) & 1ull) rank += sel[i] < em;
+  if (lane < M) {
+    const int p = below + before;
+    sorted_token[p] = lane / K;
+    sorted_expert[p] = em;
+    inv[lane] = before < cap ? p : -1;
+    if (first) active[rank] = em;
+  }
+  for (int e = lane; e < E; e += 64) {
+    int cnt = 0, less = 0;
+    for (int i = 0; i < M; ++i) {
+      const int ei = sel[i];
+      cnt += ei == e;
+      less += ei < e;
+    }
+    group_sizes[e] = cnt;
+    offsets[e] = less;
+  }
+  if (lane == 0) {
+    offsets[E] = M;
+    active[E] = __popcll(firsts);
+  }
+}
+
 }  // namespace kmoe
