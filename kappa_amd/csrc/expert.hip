@@ -877,10 +877,11 @@ constexpr int kGemmBJ = 4;                    // B loads per wave per chunk (one
 
 // Tile shapes: 128 rows with a weight ring three chunks deep (80 KB), or 160
 // rows with a ring two chunks deep (72 KB; an expert with up to 160 rows is
-// one tile). Either way two blocks fill a CU's LDS.
+// one tile): either way two blocks fill a CU's LDS. 64 rows with a ring two
+// chunks deep (48 KB): three blocks per CU.
 template <int RW>
 struct GemmShape {
-  static_assert(RW == 128 || RW == 160, "tile rows");
+  static_assert(RW == 64 || RW == 128 || RW == 160, "tile rows");
   static constexpr int kRows = RW;
   static constexpr int kA = RW * 128;          // A stage: RW rows x 64 bf16
   static constexpr int kAJ = RW / 32;          // A loads per wave per chunk (8 rows each)
@@ -1111,16 +1112,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
         gemm_tile<GATEUP, 9, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 8:
-      gemm_tile<GATEUP, 8, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      if constexpr (RW >= 128)
+        gemm_tile<GATEUP, 8, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 7:
-      gemm_tile<GATEUP, 7, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      if constexpr (RW >= 112)
+        gemm_tile<GATEUP, 7, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 6:
-      gemm_tile<GATEUP, 6, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      if constexpr (RW >= 96)
+        gemm_tile<GATEUP, 6, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 5:
-      gemm_tile<GATEUP, 5, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
+      if constexpr (RW >= 80)
+        gemm_tile<GATEUP, 5, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
     case 4:
       gemm_tile<GATEUP, 4, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
@@ -1590,11 +1595,20 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
     // with up to 128 rows per expert on average a 160-row tile is mostly the
     // expert's only one: its weights stream past the caches as well
     const bool ntb160 = big && M <= E * 128;
-    const int rw = big ? 160 : kGemmRows;
+    // 64-row tiles up to 32 rows per expert on average (48 KB of LDS, three
+    // blocks per CU, so the grid's tiles are all resident at once and stream
+    // their weights together): T = 256 / 512 159 -> 151, 169 -> 156 us per
+    // layer; at 48 and 64 rows per expert (T = 768 / 1024) an expert's rows
+    // take two tiles and it loses 9 / 18 us
+    const bool s64 = M <= E * 32;
+    const int rw = big ? 160 : (s64 ? 64 : kGemmRows);
     const int upper_mt = (M + rw - 1) / rw + slots;
     auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };
     if (stages & kStageGateUp) {
-      if (ntb)
+      if (s64)
+        hipLaunchKernelGGL((k_gemm<true, true, CH, 64>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
+                           offsets, sorted_token, w13, s13, hb, cap);
+      else if (ntb)
         hipLaunchKernelGGL((k_gemm<true, true, CH, 128>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
                            offsets, sorted_token, w13, s13, hb, cap);
       else if (ntb160)
@@ -1610,7 +1624,10 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
       if (err != hipSuccess) return err;
     }
     if (stages & kStageDown) {
-      if (ntb)
+      if (s64)
+        hipLaunchKernelGGL((k_gemm<false, true, CH, 64>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
+                           offsets, sorted_token, w2, s2, yb, cap);
+      else if (ntb)
         hipLaunchKernelGGL((k_gemm<false, true, CH, 128>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
                            offsets, sorted_token, w2, s2, yb, cap);
       else if (ntb160)

@@ -287,13 +287,17 @@ def test_30b_rows_path(dev, l30, T):
 
 
 def test_30b_skewed_routing(dev, l30):
-    for T, seed in ((4096, 7), (64, 8)):
+    """Hot experts at T=512 hold several 64-row GEMM tiles (their rows split
+    evenly over them); at T=4096 several 160-row tiles."""
+    for T, seed in ((4096, 7), (512, 9), (64, 8)):
         x = make_x(T, l30.D, seed=seed)
         x[:, 0] = 1.0
         router = skew_router(l30.router, lam=1.5)
         od = _prefill_sampled(l30, T, seed, router=router, x=x)
         share = np.sort(od["group_sizes"])[::-1][:8].sum() / (T * l30.K)
         assert share > 0.5, f"hot-expert share {share:.2f}"
+        if T == 512:
+            assert int(np.max(od["group_sizes"])) > 128
 
 
 def test_235b_layer(dev):
