@@ -168,12 +168,16 @@ bool packed_ok(const kmoe_desc& d, const kmoe_packed_experts* p) {
          p->intermediate == d.intermediate;
 }
 
-// The GEMV-style kernels up to 64 tokens (the decode batches), their row-group
-// form up to 128 tokens, the grouped GEMMs above (or whenever asked for).
+// The GEMV-style kernels up to 64 tokens (the decode batches), the grouped
+// GEMMs above (or whenever asked for). The GEMVs' row-group form covers 65 to
+// 128 tokens when the decode kernels are asked for; left to choose, the
+// grouped GEMMs (64-row tiles, every tile resident at once) are faster there:
+// T = 80 / 100 / 128 140.5 -> 136.9, 145.9 -> 136.9, 152.9 -> 137.5 us per
+// layer; at T = 40 they would lose (112.4 -> 125.6 us).
 int family_of(const kmoe_desc& d) {
   if (d.kernels == KMOE_KERNELS_GROUPED) return kmoe_host::kFamilyGemm;
   if (d.tokens <= 16 * kmoe::kDecodeMaxRowBlocks) return kmoe_host::kFamilyDecode;
-  if (d.tokens <= kmoe::kRowsPathMaxTokens) return kmoe_host::kFamilyRows;
+  if (d.kernels == KMOE_KERNELS_DECODE && d.tokens <= kmoe::kRowsPathMaxTokens) return kmoe_host::kFamilyRows;
   return kmoe_host::kFamilyGemm;
 }
 

@@ -229,16 +229,26 @@ def test_30b_decode_ragged_per_tensor(dev, l30t, T):
     _decode_full(l30t, T, "ragged", seed=80 + T)
 
 
-def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48, impl="ragged", cfg=None):
+def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48, impl="ragged", cfg=None, kernels=None):
+    """kernels: a kernel-family pin for the expert stage and the block (None:
+    the block through moe_swiglu_ffn, which chooses by T)."""
     from kappa_amd.qwen3 import moe_stages, moe_swiglu_ffn
+    from kappa_amd.qwen3.ffn_moe import _moe_forward
 
     router = layer.router if router is None else router
     x = make_x(T, layer.D, seed=seed) if x is None else x
     r, d = _route_and_dispatch(x, router, layer.E, layer.K)
     xn, idx, w, od = _check_routing(x, router, layer.E, layer.K, r, d)
-    h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl=impl)
-    out = moe_swiglu_ffn(x.reshape(1, T, layer.D), router, layer.gate, layer.up, layer.down,
-                         cfg=cfg or layer_cfg(layer, impl))  # fmt: skip
+    pin = {} if kernels is None else {"kernels": kernels}
+    h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl=impl, **pin)
+    if kernels is None:
+        out = moe_swiglu_ffn(x.reshape(1, T, layer.D), router, layer.gate, layer.up, layer.down,
+                             cfg=cfg or layer_cfg(layer, impl))  # fmt: skip
+    else:
+        out = _moe_forward(
+            x.reshape(1, T, layer.D), router, layer.gate, layer.up, layer.down, num_experts=layer.E,
+            num_experts_per_tok=layer.K, packed=None, kernels=kernels, **forward_args(impl),
+        )  # fmt: skip
     rng = np.random.default_rng(seed)
     toks = np.sort(rng.choice(T, size=min(n_tok, T), replace=False))
     toks = np.unique(np.concatenate([toks, [0, T - 1]]))
@@ -274,16 +284,21 @@ def test_30b_prefill_gather_per_tensor(dev, l30t, T):
 
 @pytest.mark.parametrize("T", [65, 100, 128])
 def test_30b_rows_path(dev, l30, T):
-    """65..128 tokens run the decode kernels over all of an expert's rows in
-    groups of 64 (the skewed router puts more than 64 rows on its hot experts,
-    so those take several groups): routing bit-exact, sampled rows and h/y
+    """65..128 tokens with the decode kernels asked for run them over all of an
+    expert's rows in groups of 64 (the skewed router puts more than 64 rows on
+    its hot experts, so those take several groups); left to choose, the same
+    sizes run the grouped GEMMs. Routing bit-exact, sampled rows and h/y
     against the oracle."""
-    _prefill_sampled(l30, T, seed=500 + T, n_tok=24)
+    from kappa_amd import _lib
+
+    for kernels in (_lib.KERNELS_DECODE, None):
+        _prefill_sampled(l30, T, seed=500 + T, n_tok=24, kernels=kernels)
     x = make_x(T, l30.D, seed=600 + T)
     x[:, 0] = 1.0
     router = skew_router(l30.router, lam=1.5)
-    od = _prefill_sampled(l30, T, seed=600 + T, router=router, x=x, n_tok=24)
-    assert int(np.max(od["group_sizes"])) > 64 or T < 100
+    for kernels in (_lib.KERNELS_DECODE, None):
+        od = _prefill_sampled(l30, T, seed=600 + T, router=router, x=x, n_tok=24, kernels=kernels)
+        assert int(np.max(od["group_sizes"])) > 64 or T < 100
 
 
 def test_30b_skewed_routing(dev, l30):
@@ -301,6 +316,7 @@ def test_30b_skewed_routing(dev, l30):
 
 
 def test_235b_layer(dev):
+    from kappa_amd import _lib
     from kappa_amd.qwen3 import moe_block_ffn, moe_stages, moe_swiglu_ffn, rms_norm
 
     layer = make_layer("235b", seed=1)
@@ -312,7 +328,7 @@ def test_235b_layer(dev):
     x40[:, 0] = 1.0
     od = _prefill_sampled(layer, 40, seed=40, n_tok=16, router=skew_router(layer.router, lam=1.5), x=x40)
     assert int(np.max(od["group_sizes"])) > 16
-    _prefill_sampled(layer, 100, seed=100, n_tok=16)  # the row-group kernels
+    _prefill_sampled(layer, 100, seed=100, n_tok=16, kernels=_lib.KERNELS_DECODE)  # the row-group kernels
     _prefill_sampled(layer, 2048, seed=2048, n_tok=24)
     # the block call at T = 100: the split router normalising 4096-wide rows
     # (four tokens per block)
@@ -445,16 +461,17 @@ def test_fused_down_combine_shapes(dev, l30, l30t, T, K, impl):
     assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
 
 
-@pytest.mark.parametrize("T", [1, 4, 8, 15, 16, 63, 64, 100, 127])
+@pytest.mark.parametrize("T", [1, 4, 8, 15, 16, 63, 100, 127])
 def test_decode_batch_invariance(dev, l30, T):
-    """A token's output does not depend on the other tokens of the call, up to
-    128 tokens: the first T rows of a (T + 1)-token call equal the T-token call
-    bit for bit. The pairs cross every kernel-shape switch below the grouped
-    GEMMs: the fused down + combine (T * K <= 32), the dense token tile of the
-    gate/up kernel (T <= 4), the one-block router finish and dispatch (T <= 16),
-    eight against four gate/up waves (T = 16/17; both sum the same eight
-    reduction parts in the same order), and the row-group kernels (T = 64/65).
-    Above 128 tokens the grouped GEMMs sum in another order."""
+    """A token's output does not depend on the other tokens of the call, on
+    either side of 64 tokens: the first T rows of a (T + 1)-token call equal
+    the T-token call bit for bit. The pairs up to 64 cross every kernel-shape
+    switch of the decode kernels: the fused down + combine (T * K <= 32), the
+    dense token tile of the gate/up kernel (T <= 4), the one-block router
+    finish and dispatch (T <= 16), and eight against four gate/up waves
+    (T = 16/17; both sum the same eight reduction parts in the same order).
+    From 65 tokens the grouped GEMMs sum each row's products in another
+    order, the same for every row and tile shape (T = 100/101, 127/128)."""
     from kappa_amd.qwen3 import moe_swiglu_ffn
 
     cfg = layer_cfg(l30, "ragged")
