@@ -1595,12 +1595,12 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
     // with up to 128 rows per expert on average a 160-row tile is mostly the
     // expert's only one: its weights stream past the caches as well
     const bool ntb160 = big && M <= E * 128;
-    // 64-row tiles up to 32 rows per expert on average (48 KB of LDS, three
+    // 64-row tiles up to 44 rows per expert on average (48 KB of LDS, three
     // blocks per CU, so the grid's tiles are all resident at once and stream
-    // their weights together): T = 256 / 512 159 -> 151, 169 -> 156 us per
-    // layer; at 48 and 64 rows per expert (T = 768 / 1024) an expert's rows
-    // take two tiles and it loses 9 / 18 us
-    const bool s64 = M <= E * 32;
+    // their weights together): T = 256 / 512 / 576 / 640 / 704 159 -> 151,
+    // 169 -> 156, 179 -> 168, 181 -> 169, 187 -> 174 us per layer; at 48 and
+    // 64 rows per expert (T = 768 / 1024) they lose 9 / 18 us
+    const bool s64 = M <= E * 44;
     const int rw = big ? 160 : (s64 ? 64 : kGemmRows);
     const int upper_mt = (M + rw - 1) / rw + slots;
     auto grid_for = [&](int NT) { return ((upper_mt * NT + 7) / 8) * 8; };

@@ -266,7 +266,7 @@ def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48, impl="ragged
     return od
 
 
-@pytest.mark.parametrize("T", [240, 512, 2048, 4096])
+@pytest.mark.parametrize("T", [240, 512, 704, 2048, 4096])
 def test_30b_prefill_ragged(dev, l30, T):
     """The prefill chunks under the reference's ragged program (ragged_jax with its
     default threshold of 64: these sizes run _moe_ragged)."""
