@@ -83,8 +83,8 @@ typedef enum kmoe_impl {
  * points; they add the same products in different f32 orders, so results agree to
  * rounding but are not bit-identical across families. */
 typedef enum kmoe_kernels {
-  KMOE_KERNELS_AUTO = 0,     /* by token count: GEMV-style up to 64 tokens, row groups up to 128, grouped GEMMs above */
-  KMOE_KERNELS_DECODE = 1,   /* the GEMV-style kernels (at most 128 tokens)           */
+  KMOE_KERNELS_AUTO = 0,     /* by token count: GEMV-style up to 64 tokens, grouped GEMMs above */
+  KMOE_KERNELS_DECODE = 1,   /* the GEMV-style kernels (at most 128 tokens; row groups above 64) */
   KMOE_KERNELS_GROUPED = 2   /* the grouped GEMMs at any token count                  */
 } kmoe_kernels;
 
