@@ -266,19 +266,23 @@ def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48, impl="ragged
     return od
 
 
-@pytest.mark.parametrize("T", [240, 512, 704, 2048, 4096])
+@pytest.mark.parametrize("T", [240, 512, 704, 1024, 1280, 2048, 4096])
 def test_30b_prefill_ragged(dev, l30, T):
     """The prefill chunks under the reference's ragged program (ragged_jax with its
-    default threshold of 64: these sizes run _moe_ragged)."""
+    default threshold of 64: these sizes run _moe_ragged). Every grouped-GEMM tile
+    form is reached: 64-row tiles (T=240, 512, 704), 128-row tiles with
+    nontemporal weights (T=1024, 64 rows per expert) and without (T=1280, 80),
+    160-row tiles with (T=2048) and without (T=4096)."""
     from kappa_amd.qwen3 import moe_layer_config
 
     cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_impl="ragged_jax")
     _prefill_sampled(l30, T, seed=100 + T, cfg=cfg)
 
 
-@pytest.mark.parametrize("T", [512, 4096])
+@pytest.mark.parametrize("T", [512, 1024, 4096])
 def test_30b_prefill_gather_per_tensor(dev, l30t, T):
-    """The gather program (the default impl) at prefill sizes on the grouped GEMMs."""
+    """The gather program (the default impl) at prefill sizes on the grouped GEMMs
+    (64-, 128- and 160-row tiles)."""
     _prefill_sampled(l30t, T, seed=150 + T, impl="gather_einsum", n_tok=24)
 
 
