@@ -3,7 +3,8 @@
     python -m kappa_amd.build            # compile every source, link kappa_amd/libkmoe.so
 
 Sources are compiled in parallel to objects under kappa_amd/_build/ and linked
-into one shared library next to this file. Every device compile disables the
+into one shared library next to this file: the HIP files with hipcc, the
+host-only validation and layout (host.cpp) with the system C++ compiler. Every device compile disables the
 packed-FP32 VALU forms (-packed-fp32-ops); hipcc's host pass warns that it does
 not know that feature, which is harmless.
 """
@@ -20,7 +21,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkmoe.so")
-SOURCES = ["api.hip", "route.hip", "expert.hip", "weights.hip", "block.hip"]
+SOURCES = ["api.hip", "route.hip", "expert.hip", "weights.hip", "block.hip", "host.cpp"]
 ARCH = os.environ.get("KMOE_OFFLOAD_ARCH", "gfx950")
 
 
@@ -51,9 +52,18 @@ def compile_flags() -> list[str]:
     ]
 
 
+def host_flags() -> list[str]:
+    """The host-only translation unit (host.cpp: validation and workspace layout)
+    is plain C++ and builds with the system compiler."""
+    return ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-I", os.path.join(ROOT, "include"), "-I", CSRC]
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *compile_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [os.environ.get("CXX", "g++"), *host_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+    else:
+        cmd = [hipcc(), *compile_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "host.h"
 #include "kmoe.h"
 
 namespace kmoe_host {
@@ -12,11 +13,6 @@ hipError_t launch_route(const kmoe_desc& d, const void* x, const kmoe_weight& ro
                         float* topk_w, int32_t* hist, hipStream_t st);
 // per-64-token-chunk expert histograms of the selections (for launch_dispatch)
 hipError_t launch_dispatch_count(const kmoe_desc& d, const int32_t* topk_idx, int32_t* hist, hipStream_t st);
-// The whole-block call routes up to this many tokens with the split router
-// (at T=256 the split router took 13 us against 21 us for k_route, whose
-// blocks then hold one token each; from 512 tokens on they are even; 240 keeps
-// every call up to 272 tokens inside the no-allocation scratch).
-constexpr int kSplitRouterMaxTokens = 240;
 // Split router (many blocks per token; same logits and selections as
 // launch_route): part holds route_split_part_floats(d) floats of workspace.
 // With a SliceNorm, x is the residual stream h: the router reduces and
@@ -40,8 +36,6 @@ struct DispatchOut {
   int32_t* sorted_expert;
   int32_t* inv;
 };
-inline bool split_router_dispatches(const kmoe_desc& d) { return d.tokens <= 16; }
-size_t route_split_part_floats(const kmoe_desc& d);
 hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part, float* logits,
                               int32_t* topk_idx, float* topk_w, hipStream_t st, const SliceNorm* norm = nullptr,
                               const DispatchOut* dispatch = nullptr);
@@ -51,21 +45,11 @@ hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weig
 // token and expert.
 hipError_t launch_route_slices(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part,
                                hipStream_t st, const SliceNorm* norm = nullptr);
-int route_split_groups(const kmoe_desc& d);
 hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const int32_t* hist, int32_t* group_sizes,
                            int32_t* offsets, int32_t* active, int32_t* sorted_token, int32_t* sorted_expert,
                            int32_t* inv, hipStream_t st);
 
 // expert.hip
-// Stage selection bits for the expert launchers.
-constexpr int kStageGateUp = 1;  // x -> h_sorted (gate/up products + SwiGLU)
-constexpr int kStageDown = 2;    // h_sorted -> y_sorted (down product)
-// Kernel families of the packed experts: the GEMV-style decode kernels (T <= 64),
-// their row-group form (T <= 128, the 30B and 235B shapes; others fall back to
-// the GEMMs), the grouped GEMMs.
-constexpr int kFamilyDecode = 0;
-constexpr int kFamilyRows = 1;
-constexpr int kFamilyGemm = 2;
 // chain: kmoe::kChainAct or kmoe::kChainF32 (common.h); with kChainF32 and bf16
 // activations h_sorted holds [T*K][2I] bf16 (the hi and lo planes of h).
 // Packed int8 experts on MFMA.

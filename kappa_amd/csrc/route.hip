@@ -602,13 +602,6 @@ struct SplitShape {
   int EPL, TB, P, Q;
 };
 
-int route_split_groups(const kmoe_desc& d) {
-  const int S = (int)((d.hidden + kRouterSlice - 1) / kRouterSlice);
-  int P = 1;
-  while (P < S) P <<= 1;
-  return P >= 4 ? P / 4 : 1;
-}
-
 static SplitShape split_shape(const kmoe_desc& d, const kmoe_weight& r) {
   SplitShape sh;
   const int E = (int)d.num_experts, T = (int)d.tokens;
@@ -621,10 +614,6 @@ static SplitShape split_shape(const kmoe_desc& d, const kmoe_weight& r) {
   while (sh.P < S) sh.P <<= 1;
   sh.Q = route_split_groups(d);
   return sh;
-}
-
-size_t route_split_part_floats(const kmoe_desc& d) {
-  return (size_t)d.tokens * route_split_groups(d) * d.num_experts;
 }
 
 template <typename A, int RT, int EPL, int TB>
