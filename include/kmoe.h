@@ -180,7 +180,7 @@ kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight
  * held until the process ends; the call allocates and frees nothing. A desc
  * whose kmoe_workspace_bytes exceeds it returns KMOE_ERR_WORKSPACE_TOO_SMALL
  * (with bf16 activations and the ragged program, the 30B-A3B layer fits up to
- * 272 tokens and the 235B-A22B layer up to 136).
+ * 291 tokens and the 235B-A22B layer up to 136).
  * Every call on one GPU shares the array: calls that overlap on a GPU (other
  * streams, other threads) race and must be serialised by the caller. */
 #define KMOE_NOALLOC_SCRATCH_BYTES (16u << 20)

@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import math
 import threading
+import warnings
 import weakref
 from collections import OrderedDict
 from dataclasses import dataclass
@@ -105,6 +106,10 @@ class PackedExperts:
     num_experts: int
     source_scale_kind: int  # _lib.SCALE_TENSOR or _lib.SCALE_CHANNEL
 
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.w13, self.s13, self.w2, self.s2))
+
     def struct(self) -> _lib.KmoePacked:
         return _lib.KmoePacked(
             self.w13.data_ptr(), self.s13.data_ptr(), self.w2.data_ptr(), self.s2.data_ptr(), self.num_experts,
@@ -176,15 +181,53 @@ class _PackCache:
     gate, up and down): it holds only weak references to them and is dropped when
     any of them is freed, so a new tensor that reuses a freed address can never
     hit an old entry. A hit also requires every source's ``_version`` to be
-    unchanged (torch in-place ops). ``max_entries`` bounds the count (least
-    recently used first out); the default holds every MoE layer of the largest
-    Qwen3 models."""
+    unchanged (torch in-place ops).
 
-    def __init__(self, max_entries: int = 256):
+    Each entry is a second copy of a layer's experts next to the caller's source
+    tensors, so the cache is bounded twice, least recently used first out:
+    ``max_entries`` entries, and ``max_bytes`` bytes of packed weights per device
+    (default: ``max_fraction`` of the device's memory). A whole large model does
+    not fit twice in one GPU (235B-A22B holds ~2.4 GB of W8 experts per layer, 94
+    layers): such models should call ``prepack_moe_experts`` once per layer at load
+    time, pass ``packed=`` and free the source int8 tensors. The first eviction
+    for lack of room warns once."""
+
+    def __init__(self, max_entries: int = 256, max_bytes: int | None = None, max_fraction: float = 0.4):
         self.max_entries = max_entries
+        self.max_bytes = max_bytes
+        self.max_fraction = max_fraction
         self._d: OrderedDict = OrderedDict()
         self._lock = threading.RLock()
         self.packs = 0  # prepack calls made (a miss)
+        self.evicted_for_room = 0
+        self._warned = False
+
+    def _budget(self, device: torch.device) -> int:
+        if self.max_bytes is not None:
+            return self.max_bytes
+        return int(self.max_fraction * torch.cuda.get_device_properties(device).total_memory)
+
+    def _device_bytes(self, device: torch.device) -> int:
+        return sum(p.nbytes for _, _, p in self._d.values() if p.w13.device == device)
+
+    def _make_room(self, device: torch.device, keep) -> None:
+        """Evict the least recently used entries of ``device`` beyond the byte budget."""
+        budget = self._budget(device)
+        while self._device_bytes(device) > budget:
+            victim = next((k for k, (_, _, p) in self._d.items() if p.w13.device == device and k != keep), None)
+            if victim is None:
+                return
+            del self._d[victim]
+            self.evicted_for_room += 1
+            if not self._warned:
+                self._warned = True
+                warnings.warn(
+                    "kappa_amd: the implicit prepack cache exceeded its budget of "
+                    f"{budget / 2**30:.1f} GiB on {device} and evicts layers, which are packed again on their next "
+                    "call; call prepack_moe_experts() at load time, pass packed= and free the source int8 tensors",
+                    ResourceWarning,
+                    stacklevel=3,
+                )
 
     @staticmethod
     def _sources(ws) -> tuple[list, tuple]:
@@ -222,6 +265,7 @@ class _PackCache:
                 weakref.finalize(t, self._evict, key)
             while len(self._d) > self.max_entries:
                 self._d.popitem(last=False)
+            self._make_room(packed.w13.device, key)
         return packed
 
     def __len__(self) -> int:
@@ -293,11 +337,15 @@ def _check_gather_scales(impl: str, ws, n_outs, E: int) -> None:
         return
     for w, n in zip(ws, n_outs):
         if is_q8_weight(w) and scale_kind(w, n, E) == _lib.SCALE_CHANNEL:
-            raise ValueError(
-                "gather_einsum takes one scale per tensor (kappa/qwen3/quant.py:71-74); per-channel scales run "
-                "with moe_impl='ragged_jax' / 'ragged_tokamax' (moe_ragged_decode_token_threshold=0 for decode "
-                "batches) or 'fixed_capacity'"
-            )
+            raise _gather_scale_error()
+
+
+def _gather_scale_error() -> ValueError:
+    return ValueError(
+        "gather_einsum takes one scale per tensor (kappa/qwen3/quant.py:71-74); per-channel scales run "
+        "with moe_impl='ragged_jax' / 'ragged_tokamax' (moe_ragged_decode_token_threshold=0 for decode "
+        "batches) or 'fixed_capacity'"
+    )
 
 
 def _moe_forward(
@@ -322,19 +370,30 @@ def _moe_forward(
     residual stream h and the call returns h + block(rms_norm(h)) (kmoe_forward_block)."""
     b, t, d = _route_checks(x, router_w, num_experts)
     E, K = num_experts, num_experts_per_tok
-    if _expert_count(ffn_gate) != E:
-        raise ValueError(f"ffn_gate has {_expert_count(ffn_gate)} experts, cfg.num_experts is {E}")
-    Eg, Dg, I = _shape(ffn_gate)
-    if Dg != d or _shape(ffn_up) != (E, d, I) or _shape(ffn_down) != (E, I, d):
-        raise ValueError(
-            f"expert shapes gate {_shape(ffn_gate)}, up {_shape(ffn_up)}, down {_shape(ffn_down)} "
-            f"do not match [E,D,I]/[E,I,D] with D={d}, E={E}"
-        )
     T = b * t
     effective = _effective_moe_impl(
         Qwen3ConfigView(impl, decode_threshold), total_tokens=T
     )  # the program that runs (kappa/qwen3/ffn_moe.py:219-223)
-    _check_gather_scales(effective, (ffn_gate, ffn_up, ffn_down), (I, I, d), E)
+    sources = (ffn_gate, ffn_up, ffn_down)
+    if any(w is None for w in sources):
+        # the packed copy alone (the source int8 tensors freed after a load-time prepack)
+        if packed is None or any(w is not None for w in sources):
+            raise ValueError("ffn_gate, ffn_up and ffn_down may be None only all together, with packed=")
+        if not isinstance(packed, PackedExperts):
+            raise ValueError(f"packed must be a PackedExperts from prepack_moe_experts (got {type(packed).__name__})")
+        I = packed.intermediate
+        if effective == "gather_einsum" and E > 1 and packed.source_scale_kind == _lib.SCALE_CHANNEL:
+            raise _gather_scale_error()
+    else:
+        if _expert_count(ffn_gate) != E:
+            raise ValueError(f"ffn_gate has {_expert_count(ffn_gate)} experts, cfg.num_experts is {E}")
+        Eg, Dg, I = _shape(ffn_gate)
+        if Dg != d or _shape(ffn_up) != (E, d, I) or _shape(ffn_down) != (E, I, d):
+            raise ValueError(
+                f"expert shapes gate {_shape(ffn_gate)}, up {_shape(ffn_up)}, down {_shape(ffn_down)} "
+                f"do not match [E,D,I]/[E,I,D] with D={d}, E={E}"
+            )
+        _check_gather_scales(effective, sources, (I, I, d), E)
     dev = x.device
     if packed is not None:
         _check_packed(packed, E, d, I, dev)
@@ -347,9 +406,14 @@ def _moe_forward(
     r, kr = weight_struct(router_w, dev, n_out=E, n_groups=None, name="router_w")
     if packed is None and packable(x.dtype, ffn_gate, ffn_up, ffn_down):
         packed = PACK_CACHE.get(ffn_gate, ffn_up, ffn_down)
-    g, kg = weight_struct(ffn_gate, dev, n_out=I, n_groups=E, name="ffn_gate")
-    u, ku = weight_struct(ffn_up, dev, n_out=I, n_groups=E, name="ffn_up")
-    dn, kd = weight_struct(ffn_down, dev, n_out=d, n_groups=E, name="ffn_down")
+    if ffn_gate is None:
+        if x.dtype != torch.bfloat16:
+            raise ValueError("packed experts alone run with bfloat16 activations")
+        g = u = dn = None
+    else:
+        g, kg = weight_struct(ffn_gate, dev, n_out=I, n_groups=E, name="ffn_gate")
+        u, ku = weight_struct(ffn_up, dev, n_out=I, n_groups=E, name="ffn_up")
+        dn, kd = weight_struct(ffn_down, dev, n_out=d, n_groups=E, name="ffn_down")
     L = _lib.lib()
     nbytes = _lib.ctypes.c_size_t()
     _lib.check(L.kmoe_workspace_bytes(desc, _lib.ctypes.byref(nbytes)))
@@ -419,7 +483,9 @@ def moe_swiglu_ffn(
 
     Shapes: ``router_w`` ``[D, E]``; ``ffn_*`` ``[E, D, I]`` / ``[E, I, D]`` for
     gate/up/down. Returns ``[B, T, D]`` in ``x.dtype``. ``packed`` optionally
-    supplies experts already relaid out by ``prepack_moe_experts``.
+    supplies experts already relaid out by ``prepack_moe_experts``; with it,
+    ``ffn_gate``, ``ffn_up`` and ``ffn_down`` may all be None (a model that
+    prepacked at load time and freed the int8 sources).
     """
     if not cfg.use_moe:
         raise ValueError("moe_swiglu_ffn requires cfg.use_moe")

@@ -200,6 +200,15 @@ def test_stage_entry_points_validate():
     i8 = weight()
     assert L.kmoe_prepack(desc(), f, i8, i8, packed(), None) == _lib.ERR_UNSUPPORTED
     assert L.kmoe_prepack(desc(), i8, i8, i8, packed(E=4), None) == _lib.ERR_INVALID_ARG
+    # the recorded kind of the source scales must be theirs: the forward calls trust
+    # it when they refuse per-channel scales under the gather program
+    pt = weight(kind=_lib.SCALE_TENSOR)
+    st, msg = status_and_msg(L.kmoe_prepack(desc(), i8, i8, i8, packed(kind=_lib.SCALE_TENSOR), None))
+    assert st == _lib.ERR_INVALID_ARG and "source_scale_kind must be CHANNEL" in msg
+    st, msg = status_and_msg(L.kmoe_prepack(desc(), pt, pt, i8, packed(kind=_lib.SCALE_TENSOR), None))
+    assert st == _lib.ERR_INVALID_ARG and "source_scale_kind must be CHANNEL" in msg
+    st, msg = status_and_msg(L.kmoe_prepack(desc(), pt, pt, pt, packed(kind=_lib.SCALE_CHANNEL), None))
+    assert st == _lib.ERR_INVALID_ARG and "source_scale_kind must be TENSOR" in msg
     assert L.kmoe_to_compute_dtype(i8, 4, 0, 1, _lib.DTYPE_BF16, 1, None) == _lib.ERR_INVALID_ARG
     assert L.kmoe_quantize_per_channel(1, 4, 4, 1, _lib.DTYPE_I8, 1, 1, None) == _lib.ERR_INVALID_ARG
 
@@ -265,3 +274,12 @@ def test_noalloc_entry_point_limits_before_any_hip_call():
     if not gpu_available():
         st, msg = status_and_msg(L.kmoe_forward_noalloc(fits, 1, f, w, w, w, None, 1, None, None, None))
         assert st == _lib.ERR_NO_DEVICE
+    # the documented limits (include/kmoe.h): 30B-A3B up to 291 tokens, 235B-A22B up to 136
+    for D, I, limit in ((2048, 768, 291), (4096, 1536, 136)):
+        over = desc(T=limit + 1, D=D, E=128, K=8, I=I)
+        st, msg = status_and_msg(L.kmoe_forward_noalloc(over, 1, f, w, w, w, None, 1, None, None, None))
+        assert st == _lib.ERR_WORKSPACE_TOO_SMALL and "scratch" in msg, (D, st, msg)
+        if not gpu_available():  # a fitting call with placeholder pointers only reaches the device check here
+            at = desc(T=limit, D=D, E=128, K=8, I=I)
+            st, msg = status_and_msg(L.kmoe_forward_noalloc(at, 1, f, w, w, w, None, 1, None, None, None))
+            assert st == _lib.ERR_NO_DEVICE, (D, st, msg)

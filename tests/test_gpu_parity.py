@@ -416,6 +416,20 @@ def test_whole_block_matches_staged_path(dev, l30, l30t, T, impl):
             assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
 
 
+@pytest.mark.parametrize("T", [4, 64, 512])
+def test_packed_experts_alone(dev, l30, T):
+    """A model that prepacked at load time passes packed= and no source weights; the
+    call runs the same kernels as with them (bit-identical)."""
+    from kappa_amd.qwen3 import moe_swiglu_ffn, prepack_moe_experts
+
+    packed = prepack_moe_experts(l30.gate, l30.up, l30.down)
+    x = make_x(T, l30.D, seed=900 + T).reshape(1, T, l30.D)
+    cfg = layer_cfg(l30, "ragged")
+    with_src = moe_swiglu_ffn(x, l30.router, l30.gate, l30.up, l30.down, cfg=cfg, packed=packed)
+    alone = moe_swiglu_ffn(x, l30.router, None, None, None, cfg=cfg, packed=packed)
+    assert torch.equal(with_src, alone)
+
+
 @pytest.mark.parametrize("T,K", [(1, 8), (2, 4), (2, 8), (3, 8), (8, 8)])
 def test_whole_block_with_drops_matches_staged_path(dev, l30, T, K):
     """Capacity 1 under a skewed router drops assignments whenever two tokens

@@ -141,8 +141,36 @@ def test_packed_argument_must_match_the_layer():
         moe_swiglu_ffn(x, r, g, u, d, cfg=c, packed=(t, t, t, t))
 
 
+def test_packed_experts_without_their_sources():
+    """After a load-time prepack the int8 sources may be freed: the expert weights are
+    then None, all three, with packed= (which then carries E, D, I and the scale kind)."""
+    from kappa_amd import _lib
+    from kappa_amd.qwen3 import PackedExperts
+
+    x, r, g, u, d = args()
+    t = torch.zeros(1)
+    c = cfg(moe_impl="ragged_jax", moe_ragged_decode_token_threshold=0)
+    p = PackedExperts(t, t, t, t, 16, 32, 8, _lib.SCALE_CHANNEL)
+    with pytest.raises(ValueError, match="None only all together"):
+        moe_swiglu_ffn(x, r, None, None, None, cfg=c)
+    with pytest.raises(ValueError, match="None only all together"):
+        moe_swiglu_ffn(x, r, None, u, d, cfg=c, packed=p)
+    with pytest.raises(ValueError, match="PackedExperts"):
+        moe_swiglu_ffn(x, r, None, None, None, cfg=c, packed=(t, t, t, t))
+    # the gather program still refuses per-channel scales, now by the packed copy's record
+    with pytest.raises(ValueError, match="gather_einsum takes one scale per tensor"):
+        moe_swiglu_ffn(x, r, None, None, None, cfg=cfg(), packed=p)
+    with pytest.raises(ValueError, match="packed experts hold"):
+        moe_swiglu_ffn(x, r, None, None, None, cfg=c, packed=PackedExperts(t, t, t, t, 32, 32, 8, _lib.SCALE_CHANNEL))
+
+
 class _FakePack:
-    pass
+    """Stands in for PackedExperts: a device (the CPU here) and a size."""
+
+    nbytes = 1000
+
+    def __init__(self):
+        self.w13 = torch.empty(0)
 
 
 @pytest.fixture
@@ -151,7 +179,7 @@ def pack_cache(monkeypatch):
     from kappa_amd.qwen3 import ffn_moe
 
     monkeypatch.setattr(ffn_moe, "prepack_moe_experts", lambda g, u, d: _FakePack())
-    return ffn_moe._PackCache()
+    return ffn_moe._PackCache(max_bytes=1 << 40)
 
 
 def _layer(seed):
@@ -205,3 +233,26 @@ def test_pack_cache_keys_on_identity_not_address(pack_cache):
     pa = pack_cache.get(*base)
     pb = pack_cache.get(*alias)
     assert pa is not pb and pack_cache.packs == 2
+
+
+def test_pack_cache_is_bounded_by_bytes_and_warns_once(pack_cache):
+    """The implicit cache doubles a layer's expert memory; past its byte budget it
+    evicts the least recently used layers (they are packed again on their next call)
+    and warns once that large models should prepack at load time."""
+    import warnings
+
+    pack_cache.max_bytes = 10 * _FakePack.nbytes
+    layers = [_layer(s) for s in range(16)]
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        for lw in layers:
+            pack_cache.get(*lw)
+    assert len(pack_cache) == 10 and pack_cache.evicted_for_room == 6
+    assert sum(issubclass(c.category, ResourceWarning) for c in caught) == 1
+    assert "prepack_moe_experts" in str(caught[0].message)
+    # the newest ten stay; the oldest is packed again
+    before = pack_cache.packs
+    pack_cache.get(*layers[-1])
+    assert pack_cache.packs == before
+    pack_cache.get(*layers[0])
+    assert pack_cache.packs == before + 1 and len(pack_cache) == 10

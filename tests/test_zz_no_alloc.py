@@ -4,17 +4,21 @@ It runs the same kernels on a workspace inside the library (a device array per
 GPU) instead of a caller's buffer, so its outputs and routing must equal
 kmoe_forward's bit for bit. Two calls in a row, the second with fewer tokens,
 check that the shared array's leftover contents from the first call do not
-leak into the second.
+leak into the second; kmoe_forward's workspace starts as all-ones bytes (NaN),
+so a read of a byte no kernel wrote would differ; the second call is also
+checked against the oracle.
 """
 
 from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import pytest
 import torch
 
-from moe_cases import make_layer, make_x
+import oracle
+from moe_cases import bf16_np, make_layer, make_x, mean_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -55,7 +59,9 @@ def _both(layer, x, impl, threshold, capacity=0):
     n = ctypes.c_size_t()
     _lib.check(L.kmoe_workspace_bytes(desc, ctypes.byref(n)))
     assert n.value <= _lib.NOALLOC_SCRATCH_BYTES
-    wsb = torch.empty(n.value, dtype=torch.uint8, device=x.device)
+    # all-ones bytes (NaN as bf16 and f32, -1 as int32): a kernel that read a
+    # workspace byte it did not write first would show in the comparison below
+    wsb = torch.full((n.value,), 0xFF, dtype=torch.uint8, device=x.device)
     stream = torch.cuda.current_stream().cuda_stream
     res = []
     for noalloc in (False, True):
@@ -89,6 +95,13 @@ def test_noalloc_equals_forward_on_two_calls(dev, impl, threshold, capacity):
         assert torch.equal(i1, i2) and torch.equal(w1, w2)
         assert torch.equal(o1, o2), f"T={T}"
         assert torch.isfinite(o2.float()).all()
+    # and the smaller call against the oracle of its program
+    h = layer.host()
+    ref = oracle.forward(bf16_np(x), h["router"], h["gate"], h["up"], h["down"], k=layer.K, act_bf16=True,
+                         impl="ragged" if impl == "ragged_jax" else impl, capacity=capacity or None)  # fmt: skip
+    np.testing.assert_array_equal(i2.cpu().numpy(), ref["idx"])
+    d = np.abs(bf16_np(o2) - ref["out"])
+    assert d.max() <= 2e-2 and mean_rel(bf16_np(o2), ref["out"]) <= 1e-3
 
 
 def test_noalloc_rejects_calls_beyond_its_scratch(dev):
