@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define KMOE_ABI_VERSION 3
+#define KMOE_ABI_VERSION 4
 
 typedef enum kmoe_status {
   KMOE_OK = 0,
@@ -215,10 +215,19 @@ kmoe_status kmoe_rms_norm(const kmoe_desc* desc, const void* x, const void* scal
 /* _route (kappa/qwen3/ffn_moe.py:38-56): logits [T,E] f32 (optional, may be
  * NULL), topk_idx [T,K] int32, topk_w [T,K] f32 holding values already
  * rounded to x.dtype, block_hist [ceil(T/64), E] int32 (per 64-token chunk
- * expert counts consumed by kmoe_dispatch). `logits_scratch` is unused (the
- * logits never leave the kernel unless `logits` is given) and may be NULL. */
+ * expert counts consumed by kmoe_dispatch). `scratch` (optional, may be NULL)
+ * of kmoe_route_scratch_bytes(desc) bytes lets a call without logits take the
+ * two-phase form when x and the router are bf16, D is 512, 1024, 2048 or
+ * 4096, E % 16 == 0 and E <= 256: every logit on the matrix cores, then the
+ * canonical order only for the experts within a rigorous f32 error bound of the
+ * K-th (the form kmoe_forward uses above 240 tokens). Selections, weights and
+ * block_hist are the same either way. */
 kmoe_status kmoe_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, float* logits,
-                       float* logits_scratch, int32_t* topk_idx, float* topk_w, int32_t* block_hist, void* stream);
+                       void* scratch, size_t scratch_bytes, int32_t* topk_idx, float* topk_w, int32_t* block_hist,
+                       void* stream);
+/* Bytes of scratch the two-phase form of kmoe_route needs (the router
+ * transposed to f32 and its column norms). */
+kmoe_status kmoe_route_scratch_bytes(const kmoe_desc* desc, size_t* bytes);
 
 /* Stable sort of assignments by expert (kappa/qwen3/ffn_moe.py:189-200, 212):
  * group_sizes [E], offsets [E+1], active [E+1] (active[0..n) = experts with

@@ -41,7 +41,7 @@ KERNELS_AUTO = 0
 KERNELS_DECODE = 1
 KERNELS_GROUPED = 2
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # kmoe_forward_noalloc's workspace (KMOE_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 16 << 20
@@ -60,6 +60,7 @@ EXPORTS = (
     "kmoe_forward_block",
     "kmoe_rms_norm",
     "kmoe_route",
+    "kmoe_route_scratch_bytes",
     "kmoe_dispatch",
     "kmoe_expert_ffn",
     "kmoe_expert_gate_up",
@@ -155,7 +156,9 @@ def _declare(L: ctypes.CDLL) -> None:
     ]  # fmt: skip
     L.kmoe_rms_norm.restype = ctypes.c_int
     L.kmoe_rms_norm.argtypes = [_DP, _P, _P, ctypes.c_int, ctypes.c_float, _P, _P]
-    L.kmoe_route.argtypes = [_DP, _P, _WP, _P, _P, _P, _P, _P, _P]
+    L.kmoe_route.argtypes = [_DP, _P, _WP, _P, _P, ctypes.c_size_t, _P, _P, _P, _P]
+    L.kmoe_route_scratch_bytes.restype = ctypes.c_int
+    L.kmoe_route_scratch_bytes.argtypes = [_DP, ctypes.POINTER(ctypes.c_size_t)]
     L.kmoe_dispatch.restype = ctypes.c_int
     L.kmoe_dispatch.argtypes = [_DP, _P, _P, _P, _P, _P, _P, _P, _P, _P]
     L.kmoe_expert_ffn.restype = ctypes.c_int

@@ -64,17 +64,24 @@ kmoe_status kmoe_device_check(void) { return device_status(); }
 
 kmoe_status kmoe_workspace_bytes(const kmoe_desc* desc, size_t* bytes) { return validate_workspace_bytes(desc, bytes); }
 
+kmoe_status kmoe_route_scratch_bytes(const kmoe_desc* desc, size_t* bytes) {
+  return validate_route_scratch_bytes(desc, bytes);
+}
+
 kmoe_status kmoe_prepack_bytes(const kmoe_desc* desc, kmoe_packed_sizes* sizes) {
   return validate_prepack_bytes(desc, sizes);
 }
 
 kmoe_status kmoe_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, float* logits,
-                       float* logits_scratch, int32_t* topk_idx, float* topk_w, int32_t* block_hist, void* stream) {
-  (void)logits_scratch;
-  KMOE_TRY(validate_route(desc, x, router, topk_idx, topk_w, block_hist));
+                       void* scratch, size_t scratch_bytes, int32_t* topk_idx, float* topk_w, int32_t* block_hist,
+                       void* stream) {
+  KMOE_TRY(validate_route(desc, x, router, scratch, scratch_bytes, topk_idx, topk_w, block_hist));
   KMOE_TRY(device_status());
   if (desc->tokens == 0) return KMOE_OK;
-  hipError_t e = launch_route(*desc, x, *router, logits, topk_idx, topk_w, block_hist, (hipStream_t)stream);
+  hipError_t e =
+      !logits && scratch && route_mfma_fits(*desc, *router)
+          ? launch_route_mfma(*desc, x, *router, scratch, topk_idx, topk_w, block_hist, (hipStream_t)stream)
+          : launch_route(*desc, x, *router, logits, topk_idx, topk_w, block_hist, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "route kernels");
   return KMOE_OK;
 }
@@ -229,7 +236,10 @@ kmoe_status forward_general(const kmoe_desc* desc, const void* x, const void* xi
       KMOE_HIP(launch_rms_norm(*desc, x, norm->scale, norm->scale_bf16 ? KMOE_DTYPE_BF16 : KMOE_DTYPE_F32,
                                           norm->eps, norm->h2, st),
                "rms_norm kernel");
-    KMOE_HIP(launch_route(*desc, xin, *router, nullptr, tidx, tw, hist, st), "route kernels");
+    if (route_mfma_preferred(*desc, *router))
+      KMOE_HIP(launch_route_mfma(*desc, xin, *router, base + w.route_part, tidx, tw, hist, st), "route kernels");
+    else
+      KMOE_HIP(launch_route(*desc, xin, *router, nullptr, tidx, tw, hist, st), "route kernels");
     KMOE_HIP(launch_dispatch(*desc, tidx, hist, gs, off, act, stok, sexp, inv, st), "dispatch kernel");
   }
   if (packed_ok(*desc, packed) && family_of(*desc) == kFamilyDecode &&

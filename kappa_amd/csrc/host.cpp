@@ -59,6 +59,26 @@ size_t route_split_part_floats(const kmoe_desc& d) {
   return (size_t)d.tokens * route_split_groups(d) * d.num_experts;
 }
 
+bool route_mfma_fits(const kmoe_desc& d, const kmoe_weight& router) {
+  const int64_t D = d.hidden;
+  return enum_value(d.act_dtype) == KMOE_DTYPE_BF16 && enum_value(router.dtype) == KMOE_DTYPE_BF16 &&
+         (D == 512 || D == 1024 || D == 2048 || D == 4096) && d.num_experts % 16 == 0 && d.num_experts <= 256;
+}
+
+bool route_mfma_preferred(const kmoe_desc& d, const kmoe_weight& router) {
+  // (layout() reserves its scratch from 2048 tokens)
+  return route_mfma_fits(d, router) && d.tokens >= 2048 && (d.hidden <= 2048 || d.tokens <= 2048);
+}
+
+size_t route_mfma_scratch_offsets(const kmoe_desc& d, int part) {
+  const size_t ED = (size_t)d.num_experts * (size_t)d.hidden;
+  const size_t o1 = align_up(2 * ED);
+  const size_t o2 = o1 + 4 * (((size_t)d.hidden + 255) / 256) * (size_t)d.num_experts;
+  return part == 1 ? o1 : (part == 2 ? o2 : 0);
+}
+
+size_t route_mfma_scratch_bytes(const kmoe_desc& d) { return route_mfma_scratch_offsets(d, 2); }
+
 bool is_float(kmoe_dtype t) {
   const int v = enum_value(t);
   return v == KMOE_DTYPE_F32 || v == KMOE_DTYPE_BF16;
@@ -170,7 +190,10 @@ Workspace layout(const kmoe_desc& d, bool block) {
   // the f32 chain keeps h as two bf16 planes per row for bf16 activations
   w.h_sorted = take((chain_of(d) == kmoe::kChainF32 && d.act_dtype == KMOE_DTYPE_BF16 ? 4 : act) * M * I);
   w.y_sorted = take(act * M * D);
-  w.route_part = take(T <= (size_t)kSplitRouterMaxTokens ? 4 * route_split_part_floats(d) : 0);
+  // the split router's group partials, or above its range the two-phase
+  // router's scratch (a bf16 router; the others need none)
+  w.route_part = take(T <= (size_t)kSplitRouterMaxTokens ? 4 * route_split_part_floats(d)
+                                                         : (T >= 2048 ? route_mfma_scratch_bytes(d) : 0));
   w.normed = take(block ? act * T * D : 0);  // rms_norm(h) for kmoe_forward_block
   w.total = o;
   return w;
@@ -326,11 +349,22 @@ kmoe_status validate_prepack_bytes(const kmoe_desc* desc, kmoe_packed_sizes* siz
   return KMOE_OK;
 }
 
-kmoe_status validate_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, const int32_t* topk_idx,
-                           const float* topk_w, const int32_t* block_hist) {
+kmoe_status validate_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, const void* scratch,
+                           size_t scratch_bytes, const int32_t* topk_idx, const float* topk_w,
+                           const int32_t* block_hist) {
   KMOE_TRY(check_desc(desc));
   KMOE_TRY(check_weight(router, "router"));
   if (!x || !topk_idx || !topk_w || !block_hist) return fail(KMOE_ERR_INVALID_ARG, "kmoe_route: NULL buffer");
+  if (scratch && scratch_bytes < route_mfma_scratch_bytes(*desc))
+    return fail(KMOE_ERR_WORKSPACE_TOO_SMALL, "kmoe_route: scratch of %zu bytes is smaller than the %zu required",
+                scratch_bytes, route_mfma_scratch_bytes(*desc));
+  return KMOE_OK;
+}
+
+kmoe_status validate_route_scratch_bytes(const kmoe_desc* desc, size_t* bytes) {
+  KMOE_TRY(check_desc(desc));
+  if (!bytes) return fail(KMOE_ERR_INVALID_ARG, "bytes is NULL");
+  *bytes = route_mfma_scratch_bytes(*desc);
   return KMOE_OK;
 }
 

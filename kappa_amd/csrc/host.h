@@ -97,6 +97,21 @@ inline int enum_value(const En& e) {
 // Split router: group partials per token and expert, and their floats.
 int route_split_groups(const kmoe_desc& d);
 size_t route_split_part_floats(const kmoe_desc& d);
+// Two-phase router (MFMA logits, canonical recompute of the candidates): the
+// shapes it takes (bf16 activations and router, D one of 512, 1024, 2048,
+// 4096, E % 16 == 0, E <= 256) and its scratch: the router transposed
+// to bf16 [E][8][D/64][8] (offset 0) and the partial sums of squares of its
+// columns [D/256][E] f32 (offset part 1); part 2 is the total.
+bool route_mfma_fits(const kmoe_desc& d, const kmoe_weight& router);
+// Whether kmoe_forward routes with it: it costs about one block's latency per
+// round of blocks (16 tokens per block up to D = 2048, 8 at D = 4096) where the
+// all-VALU k_route grows with T. Measured per layer (interleaved A/B, 30B-A3B):
+// T = 512 / 1024 / 2048 / 4096 162 -> 174, 223 -> 228, 316 -> 312, 531 -> 510 us;
+// 235B-A22B at T = 2048 915 -> 897 us; so from 2048 tokens, while D = 4096
+// grids fit one round of blocks.
+bool route_mfma_preferred(const kmoe_desc& d, const kmoe_weight& router);
+size_t route_mfma_scratch_offsets(const kmoe_desc& d, int part);
+size_t route_mfma_scratch_bytes(const kmoe_desc& d);
 
 // --- status and message ------------------------------------------------------
 // Records the message of a failing status for kmoe_last_error (per thread).
@@ -152,8 +167,10 @@ kmoe_status validate_forward_block(const kmoe_desc* desc, const void* h, const v
                                    size_t workspace_bytes, Workspace* w);
 kmoe_status validate_workspace_bytes(const kmoe_desc* desc, size_t* bytes);
 kmoe_status validate_prepack_bytes(const kmoe_desc* desc, kmoe_packed_sizes* sizes);
-kmoe_status validate_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, const int32_t* topk_idx,
-                           const float* topk_w, const int32_t* block_hist);
+kmoe_status validate_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, const void* scratch,
+                           size_t scratch_bytes, const int32_t* topk_idx, const float* topk_w,
+                           const int32_t* block_hist);
+kmoe_status validate_route_scratch_bytes(const kmoe_desc* desc, size_t* bytes);
 kmoe_status validate_dispatch(const kmoe_desc* desc, const int32_t* topk_idx, const int32_t* block_hist,
                               const int32_t* group_sizes, const int32_t* offsets, const int32_t* active,
                               const int32_t* sorted_token, const int32_t* sorted_expert, const int32_t* inv);

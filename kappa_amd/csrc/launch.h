@@ -45,6 +45,12 @@ hipError_t launch_route_split(const kmoe_desc& d, const void* x, const kmoe_weig
 // token and expert.
 hipError_t launch_route_slices(const kmoe_desc& d, const void* x, const kmoe_weight& router, float* part,
                                hipStream_t st, const SliceNorm* norm = nullptr);
+// The two-phase router (route_mfma_fits): topk_idx, topk_w and the per-64-token
+// expert histograms hist (launch_dispatch's input) from x; scratch holds
+// route_mfma_scratch_bytes(d) bytes. Same selections and weights as
+// launch_route (no logits).
+hipError_t launch_route_mfma(const kmoe_desc& d, const void* x, const kmoe_weight& router, void* scratch,
+                             int32_t* topk_idx, float* topk_w, int32_t* hist, hipStream_t st);
 hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const int32_t* hist, int32_t* group_sizes,
                            int32_t* offsets, int32_t* active, int32_t* sorted_token, int32_t* sorted_expert,
                            int32_t* inv, hipStream_t st);

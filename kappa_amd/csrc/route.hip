@@ -5,6 +5,7 @@
 #include <float.h>
 
 #include <algorithm>
+#include <cmath>
 
 #include "common.h"
 #include "launch.h"
@@ -481,6 +482,381 @@ __global__ __launch_bounds__(256) void k_dispatch_scatter(int T, int E, int K, i
                  inv, cap, L);
 }
 
+
+// ---------------------------------------------------------------------------
+// Two-phase router: bf16 activations and router, D = 64 S with S a power of
+// two from 8 to 64, E % 16 == 0, E <= 256.
+//
+// Bit-exact top-k needs the canonical logits (k_route's order) only where the
+// ranking is in doubt. Phase 1 computes every logit on the matrix cores
+// (v_mfma_f32_16x16x32_bf16: exact products, f32 sums in the hardware's order):
+// L~[t,e]. The exact sum, the canonical L and L~ differ by at most
+// c * sum_d |x_d r_de| <= c * ||x_t|| * ||r_e|| (Cauchy-Schwarz), where c covers
+// the MFMA's accumulation (taken as up to 2D roundings of up to 2u each,
+// u = 2^-24), the canonical chains and tree (64 + log2 P roundings), the
+// rounding of the norms and of L~ -/+ delta (the host passes c). So L lies in
+// [lo, hi] = [L~ - delta, L~ + delta], delta = c * ||x_t|| * ||r_e|| + 1e-30.
+// Let tau be the K-th largest lo (the search stops at 16 key bits, which can
+// only lower it). An expert whose hi is below tau has K experts strictly above
+// it and cannot be selected, ties included; the top K are among the
+// candidates {e : hi_e >= tau}. Phase 2 recomputes the candidates' logits in
+// the canonical order, ranks them (value descending, ties to the lower index)
+// and takes the softmax of the first K, as wave_topk does. A token with a
+// non-finite L~ or bound takes every expert as a candidate.
+//
+// The router is transposed once per call into rTq [E][8][S][8] bf16: element
+// (e, d = 64 s + 8 i + j) at ((e * 8 + i) * S + s) * 8 + j. Eight consecutive
+// hidden indices of one expert (an MFMA B fragment, or eight steps of a slice
+// chain) are one 16-byte load, and the 8-element pieces i of the S slices of
+// one expert are contiguous, so the slice lanes of a chain read 16 S
+// consecutive bytes per step.
+// ---------------------------------------------------------------------------
+constexpr int kRouteSliceBytes = 144;  // a 64-element bf16 slice of x in LDS, padded by 16 bytes
+
+// Block (e, p): experts 16e .. 16e+15, hidden rows 256p .. 256p+255 (slices
+// 4p .. 4p+3) of the router: rTq (exact; through LDS, so the stores are the
+// 64-byte runs of four slices of one eighth), the partial sums of squares of
+// the 16 columns npart[p][e], and the histograms zeroed. D % 256 == 0.
+__global__ __launch_bounds__(256) void k_router_prep(int D, int E, const uint16_t* __restrict__ r,
+                                                      uint16_t* __restrict__ rtq, float* __restrict__ npart,
+                                                      int32_t* __restrict__ hist, int nhist) {
+  __shared__ float red[4][16];
+  __shared__ __attribute__((aligned(16))) uint16_t tile[16 * 8 * 4 * 8];  // [e][eighth][slice][8]
+  const int e0 = blockIdx.x * 16, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nb = gridDim.x * gridDim.y, b = blockIdx.y * gridDim.x + blockIdx.x;
+  for (int i = b * 256 + tid; i < nhist; i += nb * 256) hist[i] = 0;
+  const int d = blockIdx.y * 256 + tid, S = D >> 6;
+  const uint4* row = reinterpret_cast<const uint4*>(r + (int64_t)d * E + e0);
+  const uint4 a = row[0], c = row[1];
+  const uint32_t wd[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+  const int sl = tid >> 6, i8 = (tid >> 3) & 7, j = tid & 7;
+  float sq[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t bits = (i & 1) ? (wd[i >> 1] >> 16) : (wd[i >> 1] & 0xffffu);
+    const float v = __uint_as_float(bits << 16);
+    tile[((i * 8 + i8) * 4 + sl) * 8 + j] = (uint16_t)bits;
+    sq[i] = v * v;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sq[i] += __shfl_xor(sq[i], off, 64);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) red[w][i] = sq[i];
+  }
+  __syncthreads();
+  if (tid < 16) npart[(int64_t)blockIdx.y * E + e0 + tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+  // 512 pieces of 16 bytes: piece q = (expert q / 32, eighth (q / 4) % 8, slice q % 4)
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int q = tid + 256 * k;
+    const int e = q >> 5, ei = (q >> 2) & 7, s4 = q & 3;
+    *reinterpret_cast<uint4*>(rtq + ((int64_t)((e0 + e) * 8 + ei) * S + 4 * blockIdx.y + s4) * 8) =
+        reinterpret_cast<const uint4*>(tile)[q];
+  }
+}
+
+// Order-preserving key of a float (-0.0 keyed as +0.0), as wave_topk.
+__device__ __forceinline__ uint32_t float_key(float v) {
+  const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+  return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+
+// Block: TB tokens, one wave each. The token rows are staged in LDS first
+// (slice-padded: slice s of row r at r * XRS + s * 144). Phase 1: the
+// 16-token x 16-expert logit tiles over waves (tile = w % NT, and with more
+// waves than tiles the reduction split KS ways, ks = w / NT), A from LDS, B
+// from rTq in batches of 16 steps; partial sums to LDS, and the waves of tile
+// 0 also sum the squares of their rows for ||x||. Phase 2: wave w finishes
+// token w: P lanes per candidate chain (the zero-padded slice count), 64 / P
+// chains side by side.
+template <int EPL, int P, int TB>
+__global__ __launch_bounds__(64 * TB) void k_route_mfma(int T, int D, int E, int K, const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ rtq,
+                                                         const float* __restrict__ npart, float cbound,
+                                                         int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
+                                                         int32_t* __restrict__ hist, int out_bf16) {
+  static_assert(EPL <= 4, "experts per lane");
+  constexpr int CP = 64 / P;  // chains side by side in a wave
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+  __shared__ TopkLds tk[TB];
+  __shared__ float nxp[16][16];  // [ks][row] partial sums of squares
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * TB;
+  const int S = D >> 6;
+  const int XRS = S * kRouteSliceBytes + 16;
+  const int NT = E >> 4;
+  const int KS = TB >= NT ? TB / NT : 1;
+  uint8_t* xs = lds8;
+  float* lgp = reinterpret_cast<float*>(lds8 + TB * XRS);
+  const int lgp_floats = TB * 256 > 16 * E ? TB * 256 : 16 * E;
+  int32_t* cand = reinterpret_cast<int32_t*>(lgp + lgp_floats) + w * E;
+  float* cval = reinterpret_cast<float*>(reinterpret_cast<int32_t*>(lgp + lgp_floats) + TB * E) + w * E;
+
+  // ---- phase 1 assignment: tiles tile0, tile0 + tstep, ... over steps [s0, s1) ----
+  // Step st, k-lane kq takes the 8 hidden indices of piece p = 4 st + kq, with
+  // piece p = slice p % S, eighth p / S (any one-to-one map of the reduction
+  // works when A and B follow it): the four k-lanes of an expert then read 64
+  // consecutive bytes of rTq.
+  const int m = lane & 15, kq = lane >> 4;
+  const int nsteps = D >> 5;
+  const int spk = (nsteps + KS - 1) / KS;
+  const bool split = TB >= NT;
+  // with more waves than tiles, waves past KS * NT (NT not dividing TB) sit out
+  const int tile0 = split ? (w < KS * NT ? w % NT : NT) : w;
+  const int tstep = split ? NT : TB;
+  const int ks = split ? w / NT : 0;
+  const int s0 = ks * spk, s1 = min(nsteps, s0 + spk);
+  static_assert((P & (P - 1)) == 0 && P >= 8, "slices: a power of two");
+  constexpr int LP = P == 8 ? 3 : (P == 16 ? 4 : (P == 32 ? 5 : 6));  // log2 S (S == P)
+  auto bload = [&](int tile, int st) {
+    const int p = 4 * st + kq;
+    return *reinterpret_cast<const uint4*>(rtq + ((int64_t)((16 * tile + m) * 8 + (p >> LP)) * P + (p & (P - 1))) * 8);
+  };
+  // the first batch of router fragments is requested before the token rows
+  uint4 b[8];
+  const bool pre = tile0 < NT && s1 - s0 >= 8;
+  if (pre) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) b[j] = bload(tile0, s0 + j);
+  }
+
+  // ---- the token rows into LDS (rows past T as zeros) ----
+  {
+    const int cpr = D >> 3;  // 16-byte pieces per row
+    const int per = (TB * cpr) / (64 * TB);  // per thread (D / 512, exact)
+    constexpr int PMAX = TB >= 16 ? 4 : 8;    // the host runs 16 tokens per block up to D = 2048
+    uint4 v[PMAX];
+#pragma unroll
+    for (int k = 0; k < PMAX; ++k) {
+      if (k < per) {
+        const int i = threadIdx.x + k * 64 * TB;
+        const int r = i / cpr, c = i - r * cpr;
+        v[k] = t0 + r < T ? reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * D)[c] : uint4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < PMAX; ++k) {
+      if (k < per) {
+        const int i = threadIdx.x + k * 64 * TB;
+        const int r = i / cpr, c = i - r * cpr;
+        *reinterpret_cast<uint4*>(xs + r * XRS + (c >> 3) * kRouteSliceBytes + (c & 7) * 16) = v[k];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 1 ----
+  {
+    const uint8_t* xa = xs + (m % TB) * XRS;
+    for (int tile = tile0; tile < NT; tile += tstep) {
+      const int e = 16 * tile + m;
+      floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      float ss = 0.0f;
+      auto step = [&](int st, const uint4 bb) {
+        const int p = 4 * st + kq;
+        const uint4 a = *reinterpret_cast<const uint4*>(xa + (p & (P - 1)) * kRouteSliceBytes + (p >> LP) * 16);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, bb),
+                                                      acc, 0, 0, 0);
+        if (tile == 0) {
+          const uint32_t av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float lo = __uint_as_float(av[i] << 16), hi = __uint_as_float(av[i] & 0xffff0000u);
+            ss = __builtin_fmaf(lo, lo, ss);
+            ss = __builtin_fmaf(hi, hi, ss);
+          }
+        }
+      };
+      int st = s0;
+      bool have = tile == tile0 && pre;  // b holds steps s0 .. s0 + 7
+      for (; st + 8 <= s1; st += 8) {
+        if (!have) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) b[j] = bload(tile, st + j);
+        }
+        have = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) step(st + j, b[j]);
+      }
+      for (; st < s1; ++st) step(st, bload(tile, st));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = 4 * kq + j;
+        if (row < TB) lgp[(ks * 16 + row) * E + e] = acc[j];
+      }
+      if (tile == 0) {
+        // row m's squares over this wave's reduction range: the four k-lanes of the row
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        if (kq == 0) nxp[ks][m] = ss;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: wave w, token t0 + w ----
+  const int t = t0 + w;
+  if (t >= T) return;
+  const int s = lane % P, g = lane / P;
+  float ss = 0.0f;
+  for (int k2 = 0; k2 < KS; ++k2) ss += nxp[k2][w];
+  const float nxv = sqrtf(ss);
+  const int NPD = (D + 255) >> 8;
+  float lo[EPL], hi[EPL];
+  bool bad = !(nxv <= 3.0e38f);
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    lo[i] = -INFINITY;
+    hi[i] = -INFINITY;
+    if (e < E) {
+      float v = lgp[w * E + e];
+      for (int k2 = 1; k2 < KS; ++k2) v += lgp[(k2 * 16 + w) * E + e];
+      float n2 = 0.0f;
+      for (int p = 0; p < NPD; ++p) n2 += npart[(int64_t)p * E + e];
+      const float dl = __builtin_fmaf(cbound * nxv, sqrtf(n2), 1e-30f);
+      lo[i] = v - dl;
+      hi[i] = v + dl;
+      bad = bad || !(lo[i] >= -3.0e38f && hi[i] <= 3.0e38f);
+    }
+  }
+  const bool all = __ballot(bad) != 0ull;
+  // tau: a lower bound of the K-th largest lo, to 16 key bits
+  uint32_t lk[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) lk[i] = lane + 64 * i < E ? float_key(lo[i]) : 0u;
+  uint32_t thr = 0;
+  if (!all) {
+    for (int b = 31; b >= 16; --b) {
+      const uint32_t c = thr | (1u << b);
+      int cnt = 0;
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) cnt += __popcll(__ballot(lk[i] >= c));
+      if (cnt >= K) thr = c;
+    }
+  }
+  // the candidates, in expert order
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int nc = 0;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    const bool c = e < E && (all || float_key(hi[i]) >= thr);
+    const unsigned long long mk = __ballot(c);
+    if (c) cand[nc + __popcll(mk & below)] = e;
+    nc += __popcll(mk);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // canonical logits of the candidates: lane s of a group of P runs slice s of
+  // candidates g, g + CP, ... (x[64 s ..] times r[64 s ..][e], one fmaf chain
+  // from +0), then the pairwise tree over the P slices
+  float xf[64];
+  if (s < S) {
+    const uint8_t* xrow = xs + w * XRS + s * kRouteSliceBytes;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xrow + 16 * q);
+      const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xf[8 * q + 2 * i] = __uint_as_float(wd[i] << 16);
+        xf[8 * q + 2 * i + 1] = __uint_as_float(wd[i] & 0xffff0000u);
+      }
+    }
+  }
+  for (int c = g; c < ((nc + CP - 1) / CP) * CP; c += CP) {
+    float acc = 0.0f;
+    if (s < S && c < nc) {
+      // chains past the candidates do no loads and are not stored
+      const uint4* rp = reinterpret_cast<const uint4*>(rtq + ((int64_t)cand[c] * 8 * S + s) * 8);
+      uint4 rv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) rv[i] = rp[(int64_t)i * S];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t wd[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc = __builtin_fmaf(xf[8 * i + 2 * j], __uint_as_float(wd[j] << 16), acc);
+          acc = __builtin_fmaf(xf[8 * i + 2 * j + 1], __uint_as_float(wd[j] & 0xffff0000u), acc);
+        }
+      }
+    }
+#pragma unroll
+    for (int st = 1; st < P; st <<= 1) acc = acc + __shfl_down(acc, st, P);
+    if (s == 0 && c < nc) cval[c] = acc;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (nc <= 64) {
+    // rank the candidates (value descending, ties to the lower expert; NaN as
+    // -inf), then the softmax of the first K in rank order (the sum in rank
+    // order, as wave_topk)
+    float mv = -INFINITY;
+    int me = 0x7fffffff, rank = 0;
+    if (lane < nc) {
+      const float q = cval[lane];
+      mv = q == q ? q : -INFINITY;
+      me = cand[lane];
+      for (int c = 0; c < nc; ++c) {
+        const float qc0 = cval[c];
+        const float qc = qc0 == qc0 ? qc0 : -INFINITY;
+        rank += (qc > mv) || (qc == mv && cand[c] < me);
+      }
+    }
+    if (lane < nc && rank < K) {
+      tk[w].sidx[rank] = me;
+      tk[w].key[rank] = __float_as_uint(mv);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float l0 = __uint_as_float(tk[w].key[0]);
+    const float ej = lane < K ? expf(__uint_as_float(tk[w].key[lane]) - l0) : 0.0f;
+    float ssum = 0.0f;
+    for (int j = 0; j < K; ++j) ssum = ssum + __shfl(ej, j, 64);
+    if (lane < K) {
+      const int e = tk[w].sidx[lane];
+      const float p = ej / ssum;
+      topk_w[(int64_t)t * K + lane] = out_bf16 ? round_bf16(p) : p;
+      topk_idx[(int64_t)t * K + lane] = e;
+      atomicAdd(&hist[(int64_t)(t / kDispatchBlock) * E + e], 1);
+    }
+  } else {
+    // more than 64 candidates (a token taking every expert): wave_topk over the
+    // canonical logits by expert; the candidate list is increasing in expert
+    float v[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      v[i] = -INFINITY;
+      if (e < E) {
+        int a = 0, z = nc - 1;
+        while (a < z) {
+          const int mid = (a + z) >> 1;
+          if (cand[mid] < e)
+            a = mid + 1;
+          else
+            z = mid;
+        }
+        if (cand[a] == e) {
+          const float q = cval[a];
+          v[i] = q == q ? q : -INFINITY;
+        }
+      }
+    }
+    wave_topk<EPL>(t, E, K, v, topk_idx, topk_w, out_bf16, nullptr, tk[w]);
+    if (lane < K) atomicAdd(&hist[(int64_t)(t / kDispatchBlock) * E + topk_idx[(int64_t)t * K + lane]], 1);
+  }
+}
+
 }  // namespace kmoe
 
 // ---------------------------------------------------------------------------
@@ -726,6 +1102,58 @@ hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const in
   if (!hist && nblk > 1) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_dispatch_scatter, dim3(nblk), dim3(256), 0, st, T, E, K, nblk, topk_idx, hist, group_sizes,
                      offsets, active, sorted_token, sorted_expert, inv, capacity_of(d));
+  return hipGetLastError();
+}
+
+// Two-phase router: the prep kernel (router transposed to rTq, column-norm
+// partials, histograms zeroed), then the MFMA logits, the candidates'
+// canonical logits, top-k, softmax and the per-64-token expert counts
+// (launch_dispatch reads them as it reads k_dispatch_count's).
+template <int EPL, int P, int TB>
+static void launch_route_mfma_k(const kmoe_desc& d, const uint16_t* x, const uint16_t* rtq, const float* npart,
+                                float cb, int32_t* topk_idx, float* topk_w, int32_t* hist, hipStream_t st) {
+  const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts, K = (int)d.top_k;
+  const int XRS = (D / 64) * kRouteSliceBytes + 16;
+  const int lgp = TB * 256 > 16 * E ? TB * 256 : 16 * E;
+  const size_t lds = (size_t)TB * XRS + 4 * ((size_t)lgp + 2 * (size_t)TB * E);
+  hipLaunchKernelGGL((k_route_mfma<EPL, P, TB>), dim3((T + TB - 1) / TB), dim3(64 * TB), lds, st, T, D, E, K, x, rtq,
+                     npart, cb, topk_idx, topk_w, hist, d.act_dtype == KMOE_DTYPE_BF16 ? 1 : 0);
+}
+
+// P lanes per candidate chain (the slice count rounded up to a power of two);
+// 16 tokens per block up to D = 2048, 8 above (the staged rows fit LDS).
+template <int EPL>
+static void route_mfma_p(const kmoe_desc& d, const uint16_t* x, const uint16_t* rtq, const float* npart, float cb,
+                         int32_t* topk_idx, float* topk_w, int32_t* hist, hipStream_t st) {
+  const int S = (int)(d.hidden / 64);
+  if (S <= 8) return launch_route_mfma_k<EPL, 8, 16>(d, x, rtq, npart, cb, topk_idx, topk_w, hist, st);
+  if (S <= 16) return launch_route_mfma_k<EPL, 16, 16>(d, x, rtq, npart, cb, topk_idx, topk_w, hist, st);
+  if (S <= 32) return launch_route_mfma_k<EPL, 32, 16>(d, x, rtq, npart, cb, topk_idx, topk_w, hist, st);
+  return launch_route_mfma_k<EPL, 64, 8>(d, x, rtq, npart, cb, topk_idx, topk_w, hist, st);
+}
+
+hipError_t launch_route_mfma(const kmoe_desc& d, const void* x, const kmoe_weight& r, void* scratch,
+                             int32_t* topk_idx, float* topk_w, int32_t* hist, hipStream_t st) {
+  const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts;
+  char* base = reinterpret_cast<char*>(scratch);
+  uint16_t* rtq = reinterpret_cast<uint16_t*>(base);
+  float* npart = reinterpret_cast<float*>(base + route_mfma_scratch_offsets(d, 1));
+  const int nhist = ((T + kDispatchBlock - 1) / kDispatchBlock) * E;
+  hipLaunchKernelGGL(k_router_prep, dim3(E / 16, (D + 255) / 256), dim3(256), 0, st, D, E,
+                     reinterpret_cast<const uint16_t*>(r.values), rtq, npart, hist, nhist);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  // the error bound's constant, relative to ||x|| ||r_e||: the MFMA sums as up
+  // to 2D roundings of up to 2u, the canonical chains and tree, the norms and
+  // lo / hi, with room to spare
+  const float cb = (float)std::ldexp(4.0 * D + 512.0, -24);
+  const uint16_t* xb = reinterpret_cast<const uint16_t*>(x);
+  if (E <= 64)
+    route_mfma_p<1>(d, xb, rtq, npart, cb, topk_idx, topk_w, hist, st);
+  else if (E <= 128)
+    route_mfma_p<2>(d, xb, rtq, npart, cb, topk_idx, topk_w, hist, st);
+  else
+    route_mfma_p<4>(d, xb, rtq, npart, cb, topk_idx, topk_w, hist, st);
   return hipGetLastError();
 }
 

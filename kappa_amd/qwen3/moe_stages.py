@@ -18,24 +18,37 @@ from .ffn_moe import PACK_CACHE, PackedExperts, _desc, _shape, _stream, packable
 from .quant import Weight, weight_struct
 
 
-def route(x_flat: torch.Tensor, router_w: Weight, *, num_experts: int, k: int) -> dict:
-    """Router logits [T,E] f32, top-k indices [T,K] int32, weights [T,K] f32 (rounded to x.dtype), block histogram."""
+def route(x_flat: torch.Tensor, router_w: Weight, *, num_experts: int, k: int, logits: bool = True) -> dict:
+    """Router logits [T,E] f32, top-k indices [T,K] int32, weights [T,K] f32 (rounded to x.dtype), block histogram.
+
+    logits=False: no logits; the call brings kmoe_route's scratch, so a bf16 router
+    takes the two-phase form (MFMA logits, the canonical order for the experts near
+    the K-th); the selections and weights are the same."""
     T, D = x_flat.shape
     dev = x_flat.device
     x_flat = x_flat.contiguous()
     desc = _desc(T, D, num_experts, k, 1, x_flat.dtype)
     r, keep = weight_struct(router_w, dev, n_out=num_experts, n_groups=None, name="router_w")
-    logits = torch.empty((T, num_experts), dtype=torch.float32, device=dev)
+    lg = torch.empty((T, num_experts), dtype=torch.float32, device=dev) if logits else None
     idx = torch.empty((T, k), dtype=torch.int32, device=dev)
     w = torch.empty((T, k), dtype=torch.float32, device=dev)
     hist = torch.empty(((T + 63) // 64, num_experts), dtype=torch.int32, device=dev)
+    scratch = None
+    if not logits:
+        n = _lib.ctypes.c_size_t()
+        _lib.check(_lib.lib().kmoe_route_scratch_bytes(desc, _lib.ctypes.byref(n)))
+        scratch = torch.empty(max(n.value, 1), dtype=torch.uint8, device=dev)
     _lib.check(
         _lib.lib().kmoe_route(
-            desc, x_flat.data_ptr(), r, logits.data_ptr(), None, idx.data_ptr(), w.data_ptr(), hist.data_ptr(),
-            _stream(dev),
+            desc, x_flat.data_ptr(), r, lg.data_ptr() if lg is not None else None,
+            scratch.data_ptr() if scratch is not None else None, scratch.numel() if scratch is not None else 0,
+            idx.data_ptr(), w.data_ptr(), hist.data_ptr(), _stream(dev),
         )
     )  # fmt: skip
-    return {"logits": logits, "idx": idx, "w": w, "hist": hist}
+    out = {"idx": idx, "w": w, "hist": hist}
+    if lg is not None:
+        out["logits"] = lg
+    return out
 
 
 def dispatch(idx: torch.Tensor, hist: torch.Tensor, *, num_experts: int, capacity: int = 0) -> dict:

@@ -192,10 +192,22 @@ static void forward_cases() {
 
 static void stage_cases() {
   const kmoe_desc d = desc();
-  EXPECT(validate_route(&d, P, &F, nullptr, nullptr, nullptr), KMOE_ERR_INVALID_ARG, "kmoe_route");
+  EXPECT(validate_route(&d, P, &F, nullptr, 0, nullptr, nullptr, nullptr), KMOE_ERR_INVALID_ARG, "kmoe_route");
   const int32_t* I = reinterpret_cast<const int32_t*>(P);
   const float* Fp = reinterpret_cast<const float*>(P);
-  EXPECT(validate_route(&d, P, &F, I, Fp, I), KMOE_OK, nullptr);
+  EXPECT(validate_route(&d, P, &F, nullptr, 0, I, Fp, I), KMOE_OK, nullptr);
+  size_t rs = 0;
+  EXPECT(validate_route_scratch_bytes(&d, &rs), KMOE_OK, nullptr);
+  CHECK(rs >= (size_t)2 * 8 * 128 + 4 * 8);  // the bf16 transposed router and the norm partials
+  EXPECT(validate_route(&d, P, &F, P, rs - 1, I, Fp, I), KMOE_ERR_WORKSPACE_TOO_SMALL, "scratch");
+  EXPECT(validate_route(&d, P, &F, P, rs, I, Fp, I), KMOE_OK, nullptr);
+  // the two-phase form's shapes: bf16 activations and router, 512 <= D <= 4096, D % 64, E % 16
+  const kmoe_weight RB = weight(P, KMOE_DTYPE_BF16, nullptr, KMOE_DTYPE_F32, KMOE_SCALE_NONE);
+  const kmoe_desc l30 = desc(4096, 2048, 128, 8, 768);
+  CHECK(route_mfma_fits(l30, RB) && !route_mfma_fits(l30, W) && !route_mfma_fits(desc(4096, 256, 128, 8), RB));
+  CHECK(!route_mfma_fits(desc(4096, 2048, 120, 8), RB) && !route_mfma_fits(desc(4096, 2048, 128, 8, 768, KMOE_DTYPE_F32), RB));
+  CHECK(route_mfma_preferred(l30, RB) && !route_mfma_preferred(desc(1024, 2048, 128, 8), RB));
+  CHECK(route_mfma_preferred(desc(2048, 4096, 128, 8, 1536), RB) && !route_mfma_preferred(desc(4096, 4096, 128, 8, 1536), RB));
   EXPECT(validate_dispatch(&d, I, I, I, I, I, I, I, nullptr), KMOE_ERR_INVALID_ARG, "kmoe_dispatch");
   EXPECT(validate_dispatch(&d, I, I, I, I, I, I, I, I), KMOE_OK, nullptr);
   EXPECT(validate_combine(&d, P, nullptr, Fp, P), KMOE_ERR_INVALID_ARG, "kmoe_combine");
@@ -334,7 +346,9 @@ static void layout_sweep() {
                                     f.sorted_expert, f.inv, f.h_sorted, f.y_sorted,   f.route_part, f.normed, f.total};
               const size_t need[] = {4 * M, 4 * M, 4 * nblk * E, 4 * (size_t)E, 4 * (size_t)(E + 1),
                                      4 * (size_t)(E + 1), 4 * M, 4 * M, 4 * M, hb * M * I, a * M * D,
-                                     T <= kSplitRouterMaxTokens ? 4 * route_split_part_floats(d) : 0, 0};
+                                     T <= kSplitRouterMaxTokens ? 4 * route_split_part_floats(d)
+                                                                : (T >= 2048 ? route_mfma_scratch_bytes(d) : 0),
+                                     0};
               bool ok = f.topk_idx == 0;
               for (int i = 0; i < 13; ++i) ok = ok && off[i] % 256 == 0 && off[i + 1] >= off[i] + need[i];
               CHECK(ok);

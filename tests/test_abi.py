@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_status_strings():
     L = _lib.lib()
-    assert L.kmoe_abi_version() == 3 == _lib.ABI_VERSION
+    assert L.kmoe_abi_version() == 4 == _lib.ABI_VERSION
     assert b"gfx950" in L.kmoe_version()
     for s in range(6):
         assert L.kmoe_status_string(s)
@@ -193,7 +193,12 @@ def test_packed_argument_rules():
 def test_stage_entry_points_validate():
     L = _lib.lib()
     f = weight(dtype=_lib.DTYPE_BF16, scale=None, kind=_lib.SCALE_NONE)
-    assert L.kmoe_route(desc(), 1, f, None, None, None, 1, 1, None) == _lib.ERR_INVALID_ARG
+    assert L.kmoe_route(desc(), 1, f, None, None, 0, None, 1, 1, None) == _lib.ERR_INVALID_ARG
+    # a scratch smaller than kmoe_route_scratch_bytes is refused
+    n = ctypes.c_size_t()
+    assert L.kmoe_route_scratch_bytes(desc(), ctypes.byref(n)) == _lib.OK and n.value >= 2 * 8 * 128
+    st, msg = status_and_msg(L.kmoe_route(desc(), 1, f, None, 1, n.value - 1, 1, 1, 1, None))
+    assert st == _lib.ERR_WORKSPACE_TOO_SMALL and "scratch" in msg
     assert L.kmoe_dispatch(desc(), 1, 1, 1, 1, 1, 1, 1, None, None) == _lib.ERR_INVALID_ARG
     assert L.kmoe_combine(desc(), 1, None, 1, 1, None) == _lib.ERR_INVALID_ARG
     assert L.kmoe_expert_ffn(desc(), 1, 1, 1, 1, 1, None, None, None, None, 1, 1, None) == _lib.ERR_INVALID_ARG
@@ -267,7 +272,7 @@ def test_noalloc_entry_point_limits_before_any_hip_call():
     assert L.kmoe_workspace_bytes(big, ctypes.byref(n)) == _lib.OK and n.value > _lib.NOALLOC_SCRATCH_BYTES
     st, msg = status_and_msg(L.kmoe_forward_noalloc(big, 1, f, w, w, w, None, 1, None, None, None))
     assert st == _lib.ERR_WORKSPACE_TOO_SMALL and "scratch" in msg
-    fits = desc(T=272, D=2048, E=128, K=8, I=768)
+    fits = desc(T=200, D=2048, E=128, K=8, I=768)
     assert L.kmoe_workspace_bytes(fits, ctypes.byref(n)) == _lib.OK and n.value <= _lib.NOALLOC_SCRATCH_BYTES
     st, msg = status_and_msg(L.kmoe_forward_noalloc(fits, None, f, w, w, w, None, 1, None, None, None))
     assert st == _lib.ERR_INVALID_ARG and "x and out" in msg

@@ -751,3 +751,88 @@ def test_30b_fixed_capacity(dev, l30, T, cf):
     ref = oracle.combine(yo, np.where(kept >= 0, np.arange(len(rows_t)), -1).astype(np.int32), w[toks], True,
                          impl="fixed_capacity")  # fmt: skip
     check_out(bf16_np(out.reshape(T, l30.D))[toks], ref, True, "out rows")
+
+
+# --- the two-phase router (MFMA logits, canonical recompute of the candidates) --
+
+
+def _route_two_phase_check(x, router, E, K):
+    """The two-phase router (kmoe_route with its scratch and no logits) against the
+    oracle: indices bit-exact; weights and per-64-token histograms bit-identical to
+    the all-VALU form (same canonical logits, same expf)."""
+    from kappa_amd.qwen3 import moe_stages
+
+    r2 = moe_stages.route(x, router, num_experts=E, k=K, logits=False)
+    r1 = moe_stages.route(x, router, num_experts=E, k=K)
+    assert "logits" not in r2
+    lg = oracle.router_logits(bf16_np(x), router.float().cpu().numpy())
+    np.testing.assert_array_equal(r1["logits"].cpu().numpy(), lg)
+    idx, _ = oracle.topk_softmax(lg, K, act_bf16=True)
+    np.testing.assert_array_equal(r2["idx"].cpu().numpy(), idx)
+    np.testing.assert_array_equal(r2["idx"].cpu().numpy(), r1["idx"].cpu().numpy())
+    np.testing.assert_array_equal(r2["w"].cpu().numpy(), r1["w"].cpu().numpy())
+    np.testing.assert_array_equal(r2["hist"].cpu().numpy(), r1["hist"].cpu().numpy())
+    return lg, idx
+
+
+@pytest.mark.parametrize("T", [241, 512, 1000, 4096])
+def test_two_phase_router_30b(dev, l30, T):
+    """The prefill sizes of the 30B-A3B layer, uniform and Zipf-skewed routing."""
+    x = make_x(T, l30.D, seed=1200 + T)
+    _route_two_phase_check(x, l30.router, l30.E, l30.K)
+    x[:, 0] = 1.0
+    _route_two_phase_check(x, skew_router(l30.router, lam=1.5), l30.E, l30.K)
+
+
+@pytest.mark.parametrize("D,E,K,T", [(4096, 128, 8, 300), (4096, 128, 8, 2048), (1024, 64, 4, 333), (512, 256, 8, 700)])
+def test_two_phase_router_shapes(dev, D, E, K, T):
+    """The 235B-A22B router (64 slices per candidate) and other slice counts and
+    expert counts (the kernel's template forms)."""
+    g = torch.Generator(device="cuda").manual_seed(D + E + T)
+    router = (torch.randn(D, E, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    x = make_x(T, D, seed=1300 + T)
+    _route_two_phase_check(x, router, E, K)
+
+
+def test_two_phase_router_ties_near_ties_and_fallback(dev):
+    """Exact ties straddling the K-th place on every token (experts in groups of three
+    identical router columns: the top K = 8 ends inside a group), near ties (copies
+    that differ in one entry by one bf16 ulp), an all-zero row (all logits 0: the
+    first K experts, weights 1/K) and rows whose norm overflows f32 (the token takes
+    every expert as a candidate); the oracle's tie rule is the lower index first."""
+    D, E, K, T = 2048, 128, 8, 600
+    g = torch.Generator(device="cuda").manual_seed(77)
+    base = (torch.randn(D, 43, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    router = base[:, torch.arange(E, device="cuda") % 43].contiguous()
+    x = make_x(T, D, seed=1400)
+    _route_two_phase_check(x, router, E, K)
+    near = router.clone()
+    for e in range(43, E):  # each copy one ulp away from its source in one entry
+        dd = (e * 37) % D
+        bits = near[dd, e].view(torch.int16)
+        near[dd, e] = (bits + 1).view(torch.bfloat16)
+    x[0] = 0.0
+    x[1] = x[1] * 2.0**100  # ||x||^2 overflows f32; the logits stay finite
+    x[2, ::3] = 0.0
+    lg, idx = _route_two_phase_check(x, near, E, K)
+    np.testing.assert_array_equal(idx[0], np.arange(K))
+    assert np.isfinite(lg[1]).all()
+
+
+@pytest.mark.parametrize("T", [512, 2048, 4096])
+def test_forward_routing_two_phase(dev, l30, T):
+    """kmoe_forward from 2048 tokens routes with the two-phase form (below, the
+    all-VALU router): its indices and weights equal the stage router's."""
+    from kappa_amd.qwen3 import moe_stages
+    from kappa_amd.qwen3.ffn_moe import _moe_forward
+
+    x = make_x(T, l30.D, seed=1500 + T)
+    _, idx, w = _moe_forward(
+        x.reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, num_experts=l30.E,
+        num_experts_per_tok=l30.K, packed=None, return_routing=True, **forward_args("ragged"),
+    )  # fmt: skip
+    r = moe_stages.route(x, l30.router, num_experts=l30.E, k=l30.K)
+    lg = oracle.router_logits(bf16_np(x), l30.router.float().cpu().numpy())
+    oidx, _ = oracle.topk_softmax(lg, l30.K, act_bf16=True)
+    np.testing.assert_array_equal(idx.cpu().numpy(), oidx)
+    assert torch.equal(w.float(), r["w"])
