@@ -401,6 +401,42 @@ def prefill_point(layers, T, args, dev, router_fn=None, roofline=False, seed=11)
     return res
 
 
+def near_ties(router, xs, K, exact_products=True):
+    """Tokens whose canonical K-th / (K+1)-th logit gap another fp32 summation order
+    could close (the reference sums the router product in XLA's order,
+    kappa/qwen3/ffn_moe.py:50): any order of the D products is within
+    gamma * S_e of the exact sum, S_e = sum_d |x_d r_de|, gamma = n u / (1 - n u),
+    u = 2^-24, n = D (D + 1 when the products round: f32 inputs); two orders are
+    within 2 gamma S_e of each other. A token with gap <= 2 gamma (S_K + S_K+1) may
+    select a different K-th expert under XLA's order; the others cannot."""
+    import torch
+
+    from kappa_amd.qwen3 import moe_stages
+
+    D, E = router.shape
+    n = D if exact_products else D + 1
+    u = 2.0**-24
+    gamma = n * u / (1.0 - n * u)
+    within, total, worst, differs = 0, 0, float("inf"), 0
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    for x in xs:
+        lg = moe_stages.route(x, router, num_experts=E, k=K)["logits"]
+        S = x.abs().float() @ router.abs().float()
+        vals, order = torch.sort(lg, dim=1, descending=True, stable=True)
+        gap = (vals[:, K - 1] - vals[:, K]).double()
+        bound = 2.0 * gamma * (S.gather(1, order[:, K - 1 : K]) + S.gather(1, order[:, K : K + 1])).double()[:, 0]
+        within += int((gap <= bound).sum())
+        total += x.shape[0]
+        worst = min(worst, float((gap / bound).min()))
+        # the same products summed in another order: torch's f32 GEMM
+        alt = torch.sort(x.float() @ router.float(), dim=1, descending=True, stable=True)[1][:, :K]
+        differs += int((alt != order[:, :K]).any(dim=1).sum())
+    torch.backends.cuda.matmul.allow_tf32 = prev
+    return {"tokens": total, "within_order_bound": within, "min_gap_over_bound": worst,
+            "topk_differs_under_f32_gemm_order": differs}  # fmt: skip
+
+
 def library_reference(T, D, I, E, K, reps=10):
     """hipBLASLt (torch.bmm, bf16) on the prefill expert shapes with uniform
     routing, M = T*K/E rows per expert, bf16 weights (no int8 conversion, no
@@ -501,6 +537,10 @@ def bench_235b(args, dev):
     log("bench: building 2 weight copies of the 235B-A22B W8 layer")
     big = [make_layer("235b", seed=40 + i) for i in range(2)]
     res = {"decode_T16": decode_point(big, 16, args, dev), "prefill_T2048": prefill_point(big, 2048, args, dev)}
+    res["routing_near_ties"] = {
+        "decode_T16": near_ties(big[0].router, make_x_list(16, big[0].D, 8, 7 + 16, dev), big[0].K),
+        "prefill_T2048": near_ties(big[0].router, make_x_list(2048, big[0].D, 2, 11 + 2048, dev), big[0].K),
+    }
     for v in res.values():
         v.pop("_gate_up_bytes", None)
     del big
@@ -683,6 +723,26 @@ def main():
         del gl
         if "prefill" in result:
             result["prefill"]["library_reference"] = library_reference(4096, D, I, E, K)
+
+    if not args.quick:
+        # routing near ties against another summation order, per BASELINE config
+        # (the inputs of the timed points above)
+        from inputs import GOLDEN_SPECS, make_inputs
+
+        margins = {}
+        for Td in dall:
+            margins[f"30b_decode_T{Td}"] = near_ties(lay0.router, make_x_list(Td, D, 8, 7 + Td, dev), K)
+        for Tp in sorted({int(v) for v in args.prefill.split(",") if v}):
+            margins[f"30b_prefill_T{Tp}"] = near_ties(lay0.router, make_x_list(Tp, D, 2, 11 + Tp, dev), K)
+        sr = skew_router(lay0.router, lam=1.5)
+        margins["30b_skew_decode_T64"] = near_ties(sr, make_x_list(64, D, 8, 7 + 64, dev, skew=True), K)
+        margins["30b_skew_prefill_T4096"] = near_ties(sr, make_x_list(4096, D, 2, 11 + 4096, dev, skew=True), K)
+        toy = next(sp for sp in GOLDEN_SPECS if sp.name == "toy_f32")
+        ti = make_inputs(toy)
+        margins["toy_f32_T64"] = near_ties(torch.from_numpy(ti["router"]).to(dev), [torch.from_numpy(ti["x"]).to(dev)],
+                                           toy.K, exact_products=False)  # fmt: skip
+        result["routing_near_ties"] = margins
+        log(f"bench: routing near ties {margins}")
 
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle)")

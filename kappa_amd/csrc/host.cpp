@@ -67,7 +67,7 @@ bool route_mfma_fits(const kmoe_desc& d, const kmoe_weight& router) {
 
 bool route_mfma_preferred(const kmoe_desc& d, const kmoe_weight& router) {
   // (layout() reserves its scratch from 2048 tokens)
-  return route_mfma_fits(d, router) && d.tokens >= 2048 && (d.hidden <= 2048 || d.tokens <= 2048);
+  return route_mfma_fits(d, router) && d.tokens >= 2048;
 }
 
 size_t route_mfma_scratch_offsets(const kmoe_desc& d, int part) {

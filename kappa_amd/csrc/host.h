@@ -105,10 +105,13 @@ size_t route_split_part_floats(const kmoe_desc& d);
 bool route_mfma_fits(const kmoe_desc& d, const kmoe_weight& router);
 // Whether kmoe_forward routes with it: it costs about one block's latency per
 // round of blocks (16 tokens per block up to D = 2048, 8 at D = 4096) where the
-// all-VALU k_route grows with T. Measured per layer (interleaved A/B, 30B-A3B):
-// T = 512 / 1024 / 2048 / 4096 162 -> 174, 223 -> 228, 316 -> 312, 531 -> 510 us;
-// 235B-A22B at T = 2048 915 -> 897 us; so from 2048 tokens, while D = 4096
-// grids fit one round of blocks.
+// all-VALU k_route grows with T. Alone, with the router in cache, k_route wins
+// up to ~2300 tokens at D = 2048 and ~4000 at D = 4096; inside the layer, where
+// the expert GEMMs have evicted the router, whole layers with the one-phase and
+// the two-phase router (two interleaved rounds) ran 30B-A3B T = 2048 / 2560 /
+// 3072 / 4096 310 / 386 / 436 / 519 against 311 / 376 / 435 / 505 us, 235B-A22B
+// T = 2048 / 3072 / 4096 874 / 1350 / 1696 against 873 / 1338 / 1668 us: even at
+// 2048 tokens, ahead above, for both widths.
 bool route_mfma_preferred(const kmoe_desc& d, const kmoe_weight& router);
 size_t route_mfma_scratch_offsets(const kmoe_desc& d, int part);
 size_t route_mfma_scratch_bytes(const kmoe_desc& d);

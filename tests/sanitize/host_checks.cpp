@@ -207,7 +207,8 @@ static void stage_cases() {
   CHECK(route_mfma_fits(l30, RB) && !route_mfma_fits(l30, W) && !route_mfma_fits(desc(4096, 256, 128, 8), RB));
   CHECK(!route_mfma_fits(desc(4096, 2048, 120, 8), RB) && !route_mfma_fits(desc(4096, 2048, 128, 8, 768, KMOE_DTYPE_F32), RB));
   CHECK(route_mfma_preferred(l30, RB) && !route_mfma_preferred(desc(1024, 2048, 128, 8), RB));
-  CHECK(route_mfma_preferred(desc(2048, 4096, 128, 8, 1536), RB) && !route_mfma_preferred(desc(4096, 4096, 128, 8, 1536), RB));
+  CHECK(route_mfma_preferred(desc(2048, 4096, 128, 8, 1536), RB) && route_mfma_preferred(desc(4096, 4096, 128, 8, 1536), RB));
+  CHECK(!route_mfma_preferred(desc(2047, 4096, 128, 8, 1536), RB) && !route_mfma_preferred(desc(4096, 4096, 128, 8, 1536, KMOE_DTYPE_F32), RB));
   EXPECT(validate_dispatch(&d, I, I, I, I, I, I, I, nullptr), KMOE_ERR_INVALID_ARG, "kmoe_dispatch");
   EXPECT(validate_dispatch(&d, I, I, I, I, I, I, I, I), KMOE_OK, nullptr);
   EXPECT(validate_combine(&d, P, nullptr, Fp, P), KMOE_ERR_INVALID_ARG, "kmoe_combine");
