@@ -548,6 +548,79 @@ def bench_235b(args, dev):
     return res
 
 
+def floor_probe():
+    """What a kernel costs before it does any work, and how fast a cold stream of
+    the T=1 layer's weight sizes moves, on this device: a one-element fill (one
+    block) launched 200 times back to back, eagerly and from a graph; and
+    elementwise passes (bitwise not: one read and one write per byte, a launch
+    grid per size) whose sources rotate over enough buffers (> 256 MB) that every
+    pass reads from HBM, with the traffic of the T=1 layer's weights (12.6 MB,
+    the down weights of 8 experts; 25.2 MB, their gate and up weights; 37.7 MB,
+    all three)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    t = torch.zeros(1, device=dev)
+
+    def per_launch(fn, n=200, graph=False):
+        if graph:
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                fn()
+                torch.cuda.synchronize()
+                with torch.cuda.graph(g, stream=s):
+                    for _ in range(n):
+                        fn()
+            torch.cuda.current_stream().wait_stream(s)
+            run = g.replay
+        else:
+
+            def run():
+                for _ in range(n):
+                    fn()
+
+        run()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            run()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / n)
+        return best
+
+    res = {
+        "fill_1_element_us_eager": per_launch(lambda: t.fill_(1.0)),
+        "fill_1_element_us_graph": per_launch(lambda: t.fill_(1.0), graph=True),
+        "cold_stream": {},
+    }
+    for mb, what in ((12.6, "down weights of 8 experts"), (25.2, "gate/up weights of 8 experts"),
+                     (37.7, "all weights of 8 experts")):  # fmt: skip
+        n = int(mb * 1e6 / 2) // 256 * 256  # n bytes read and n written
+        nbuf = max(2, int(400e6 // n) + 1)
+        srcs = [torch.full((n,), i, dtype=torch.uint8, device=dev) for i in range(nbuf)]
+        dst = torch.empty(n, dtype=torch.uint8, device=dev)
+        times = []
+        for r in range(3 * nbuf):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            torch.bitwise_not(srcs[r % nbuf], out=dst)
+            e1.record()
+            torch.cuda.synchronize()
+            if r >= nbuf:
+                times.append(e0.elapsed_time(e1) * 1e3)
+        times.sort()
+        us = times[len(times) // 2]
+        res["cold_stream"][f"{mb}MB"] = {"traffic_bytes": 2 * n, "us": us, "GBps": 2 * n / us / 1e3, "as": what}
+        del srcs, dst
+    log(f"bench: floor {res}")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -573,6 +646,12 @@ def main():
         help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that scales the "
         "FETCH_SIZE / WRITE_SIZE counters) and exit",
     )
+    ap.add_argument(
+        "--floor",
+        action="store_true",
+        help="only time the floors the small decode batches are measured against (a one-block kernel, "
+        "back to back and in a graph; cold streams of the T=1 layer's weight sizes) and exit",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -593,6 +672,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"bench: 5 copies of {args.copy_calibration} MiB ({n} bytes read and written each)")
+        return
+
+    if args.floor:
+        print(json.dumps({"floor": floor_probe()}), flush=True)
         return
 
     from kappa_amd import _lib
