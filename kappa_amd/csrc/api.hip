@@ -35,11 +35,11 @@ kmoe_status device_status() {
 kmoe_status expert_stage(const kmoe_desc& d, int stages, const void* x, const int32_t* offsets, const int32_t* active,
                          const int32_t* sorted_token, const int32_t* sorted_expert, const kmoe_weight* gate,
                          const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed,
-                         void* h_sorted, void* y_sorted, hipStream_t st) {
+                         void* h_sorted, void* y_sorted, hipStream_t st, float* h_scale = nullptr) {
   hipError_t e;
   if (packed_ok(d, packed)) {
     e = launch_expert_packed(d, chain_of(d), family_of(d), stages, x, offsets, active, sorted_token, *packed,
-                             h_sorted, y_sorted, st);
+                             h_sorted, y_sorted, st, h_scale);
   } else {
     e = launch_expert_generic(d, chain_of(d), stages, x, sorted_token, sorted_expert, gate, up, down, h_sorted,
                               y_sorted, st);
@@ -250,8 +250,11 @@ kmoe_status forward_general(const kmoe_desc* desc, const void* x, const void* xi
     KMOE_HIP(launch_down_combine(*desc, chain, scatter, hs, tidx, inv, tw, *packed, out, st, res),
              "down+combine kernel");
   } else {
+    // with down_planes_fits the workspace's h rows become int8 planes, their
+    // scales in w.h_scale
+    float* hscale = down_planes_fits(*desc) ? reinterpret_cast<float*>(base + w.h_scale) : nullptr;
     KMOE_TRY(expert_stage(*desc, kStageGateUp | kStageDown, xin, off, act, stok, sexp, gate,
-                          up, down, packed, hs, ys, st));
+                          up, down, packed, hs, ys, st, hscale));
     KMOE_HIP(launch_combine(*desc, scatter, ys, inv, tw, out, st, res), "combine kernel");
   }
   return KMOE_OK;

@@ -874,19 +874,23 @@ __device__ __forceinline__ int a_swz(int r, int p) { return r * 64 + (a_piece(r,
 constexpr int kGemmRows = 128;                // rows per tile (the 128-row form)
 constexpr int kGemmB = 16 * 1024;             // B stage: 16 cells x 64 k x 16 columns int8
 constexpr int kGemmBJ = 4;                    // B loads per wave per chunk (one cell each)
+// weight ring depth of the int8-plane down product: two chunks (48 KB, three
+// blocks per CU); three (64 KB, two blocks) ran 30B-A3B T = 4096 476 -> 492 us
+// and 235B-A22B T = 2048 813 -> 823 us per layer
+constexpr int kI8Ring = 2;
 
 // Tile shapes: 128 rows with a weight ring three chunks deep (80 KB), or 160
 // rows with a ring two chunks deep (72 KB; an expert with up to 160 rows is
 // one tile): either way two blocks fill a CU's LDS. 64 rows with a ring two
 // chunks deep (48 KB): three blocks per CU.
-template <int RW>
+template <int RW, int NB = 0>
 struct GemmShape {
   static_assert(RW == 64 || RW == 128 || RW == 160, "tile rows");
   static constexpr int kRows = RW;
   static constexpr int kA = RW * 128;          // A stage: RW rows x 64 bf16
   static constexpr int kAJ = RW / 32;          // A loads per wave per chunk (8 rows each)
   static constexpr int kNA = 2;                // A ring depth
-  static constexpr int kNB = RW == 128 ? 3 : 2;  // B ring depth
+  static constexpr int kNB = NB ? NB : (RW == 128 ? 3 : 2);  // B ring depth
   static constexpr int kLds = kNA * kA + kNB * kGemmB;
 };
 
@@ -1026,18 +1030,119 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads<GemmSha
   }
 }
 
+// The kChainF32 down product on integer planes (k_gemm with I8): A rows are h's
+// two int8 digit planes (k_h_planes), B the packed int8 weights as they are, on
+// v_mfma_i32_16x16x64_i8 (lane l: row / column l % 16, k = 16 (l / 16) .. + 15,
+// the layout of a packed 16-byte piece). A chunk is 64 k of both planes: a row's
+// 128 bytes at chunk offset c * 128 (plane 0 in pieces 0..3, plane 1 in 4..7),
+// the bytes of a bf16 chunk, so the A ring, its swizzle and its loads are the
+// PL = 1 ones. The planes accumulate exactly in i32 (|sum| <= I * 127 * 128);
+// the epilogue forms 256 a1 + a2 in f32 and applies the row's scale (a power of
+// two) and the column's.
+template <int MT, bool NTB, int RW>
+__device__ __forceinline__ void gemm_tile_i8(uint8_t* smem, const GemmLoads<GemmShape<RW>::kAJ>& gl, int KC, int wv,
+                                             int rows, int row0, int nt, const uint16_t* __restrict__ src,
+                                             const float* __restrict__ hs, uint16_t* __restrict__ dst, int Ndim) {
+  using Sh = GemmShape<RW, kI8Ring>;
+  constexpr int kGemmA = Sh::kA, kGemmAJ = Sh::kAJ, kGemmNA = Sh::kNA, kGemmNB = Sh::kNB;
+  const int lane = threadIdx.x & 63;
+  const uint32_t lds0 = lds_addr(smem);
+  const uint8_t* const bring = smem + kGemmNA * kGemmA;
+  int32x4 a1c[MT][4], a2c[MT][4];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      a1c[mi][g] = int32x4{0, 0, 0, 0};
+      a2c[mi][g] = int32x4{0, 0, 0, 0};
+    }
+  auto issue_a = [&](int c) {
+    const uint32_t st = lds0 + (uint32_t)((c & 1) * kGemmA + wv * kGemmAJ * 1024);
+    const uint16_t* abase = src + c * 64;
+#pragma unroll
+    for (int j = 0; j < kGemmAJ; ++j) dma16(gl.avoff[j], abase, st + j * 1024);
+  };
+  auto issue_b = [&](int b) {
+    const uint32_t st = lds0 + (uint32_t)(kGemmNA * kGemmA + (b % kGemmNB) * kGemmB + wv * 4096);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (NTB)
+        dma16_stream(lane * 16, gl.bsrc[g] + b * 1024, st + g * 1024);
+      else
+        dma16(lane * 16, gl.bsrc[g] + b * 1024, st + g * 1024);
+    }
+  };
+  // the PL = 1 schedule of gemm_tile: kAhead weight chunks issued ahead
+  constexpr int kAhead = kGemmNB == 3 ? 2 : 1;
+  issue_b(0);
+  issue_a(0);
+  if (kAhead == 2 && 1 < KC) {
+    issue_b(1);
+    vm_barrier<kGemmBJ>();
+  } else {
+    vm_barrier<0>();
+  }
+  for (int c = 0; c < KC; ++c) {
+    bool b_ahead = false;
+    if (c + 1 < KC) issue_a(c + 1);
+    if (c + kAhead < KC) {
+      issue_b(c + kAhead);
+      b_ahead = kAhead == 2;
+    }
+    int32x4 q[4];
+    const uint8_t* bp = bring + (c % kGemmNB) * kGemmB + wv * 4096 + lane * 16;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[g] = *reinterpret_cast<const int32x4*>(bp + g * 1024);
+    const uint16_t* As = reinterpret_cast<const uint16_t*>(smem + (c & 1) * kGemmA);
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+      const int r = mi * 16 + (lane & 15);
+      const int32x4 p1 = *reinterpret_cast<const int32x4*>(As + a_swz(r, lane >> 4));
+      const int32x4 p2 = *reinterpret_cast<const int32x4*>(As + a_swz(r, 4 + (lane >> 4)));
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        a1c[mi][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p1, q[g], a1c[mi][g], 0, 0, 0);
+        a2c[mi][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p2, q[g], a2c[mi][g], 0, 0, 0);
+      }
+    }
+    if (c + 1 < KC) {
+      if (b_ahead)
+        vm_barrier<kGemmBJ>();
+      else
+        vm_barrier<0>();
+    }
+  }
+  // epilogue: lane holds rows 4*(lane/16)+j of each 16x16 tile, column lane%16
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = mi * 16 + 4 * (lane >> 4) + j;
+      if (row >= rows) continue;
+      const float rs = hs[row0 + row];
+      uint16_t* drow = dst + (size_t)(row0 + row) * Ndim;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float v = __fadd_rn(__fmul_rn((float)a1c[mi][g][j], 256.0f), (float)a2c[mi][g][j]);
+        drow[nt * 256 + wv * 64 + g * 16 + (lane & 15)] = f32_to_bf16_bits(__fmul_rn(__fmul_rn(v, rs), gl.sc[g]));
+      }
+    }
+  }
+}
+
 // GATEUP = true: A rows gathered from x by token, B = gate|up cells, epilogue
 // SwiGLU -> h_sorted. GATEUP = false: A = h_sorted rows, B = down, epilogue ->
 // y_sorted. src must span fewer than 2^32 bytes (32-bit load offsets).
 // NTB: the weights are loaded with the nontemporal hint (few rows per expert,
 // so no second row tile would find them in L2).
-template <bool GATEUP, bool NTB, int CH, int RW>
+template <bool GATEUP, bool NTB, int CH, int RW, bool I8 = false>
 __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint16_t* __restrict__ src,
                                                   const int32_t* __restrict__ offsets,
                                                   const int32_t* __restrict__ sorted_token,
                                                   const int8_t* __restrict__ wp, const float* __restrict__ sp,
-                                                  uint16_t* __restrict__ dst, int cap) {
-  using Sh = GemmShape<RW>;
+                                                  uint16_t* __restrict__ dst, int cap, const float* __restrict__ hs) {
+  static_assert(!I8 || (!GATEUP && CH == kChainF32 && RW == 64), "int8 planes: the f32 chain's down product");
+  using Sh = GemmShape<RW, I8 ? kI8Ring : 0>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Sh::kLds];
   // set-up scratch inside the ring (no loads are in flight yet)
   int* const mtp = reinterpret_cast<int*>(smem);
@@ -1100,7 +1205,24 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   // wave may start loading into the ring while another still reads tok
   asm volatile("" ::"v"(gl.sc[0]), "v"(gl.sc[1]), "v"(gl.sc[2]), "v"(gl.sc[3]));
   __syncthreads();
-  constexpr int PL = !GATEUP && CH == kChainF32 ? 2 : 1;  // h planes of the down product
+  constexpr int PL = !GATEUP && CH == kChainF32 && !I8 ? 2 : 1;  // h planes of the down product
+  if constexpr (I8) {
+    switch ((rows + 15) >> 4) {
+      case 4:
+        gemm_tile_i8<4, NTB, RW>(smem, gl, KCW, wv, rows, row0, nt, src, hs, dst, Ndim);
+        break;
+      case 3:
+        gemm_tile_i8<3, NTB, RW>(smem, gl, KCW, wv, rows, row0, nt, src, hs, dst, Ndim);
+        break;
+      case 2:
+        gemm_tile_i8<2, NTB, RW>(smem, gl, KCW, wv, rows, row0, nt, src, hs, dst, Ndim);
+        break;
+      default:
+        gemm_tile_i8<1, NTB, RW>(smem, gl, KCW, wv, rows, row0, nt, src, hs, dst, Ndim);
+        break;
+    }
+    return;
+  }
   // as many 16-row MFMA tiles as the rows need
   switch ((rows + 15) >> 4) {
     case 10:
@@ -1140,6 +1262,73 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
       gemm_tile<GATEUP, 1, NTB, CH, PL, RW>(smem, gl, KCW, wv, rows, row0, nt, src, dst, Ndim);
       break;
   }
+}
+
+// The f32 chain's h for the integer down product: row m's hi and lo planes
+// (h = hi + lo, exact in f32) become two int8 digit planes of the integer
+// H = rint(h * 2^k), H = 256 p1 + p2 with p2 in [-128, 127] and p1 in
+// [-127, 127]; k is the largest power of two with max |h| * 2^k <= 32639, so H
+// keeps 15 bits relative to the row's largest |h|. In place: the planes take
+// the first 2I bytes of the row (chunk c: p1 at c * 128, p2 at c * 128 + 64)
+// once the wave holds the whole row; hs[m] = 2^-k. A row with a non-finite h
+// gets hs[m] = NaN, so its whole y row is NaN. One wave per row, I <= 2048.
+__global__ __launch_bounds__(256) void k_h_planes(int M, int I, uint16_t* __restrict__ h, float* __restrict__ hs) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  uint16_t* row = h + (size_t)m * 2 * I;
+  // lane L, step s: the four elements from 4 (L + 64 s) on (8-byte loads of
+  // each bf16 plane, 4-byte stores of each int8 plane)
+  constexpr int kSteps = kPlanesMaxChunks / 4;
+  float v[kSteps][4];
+  float mx = 0.0f;
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const int e = 4 * (lane + 64 * st);
+    if (e < I) {
+      const uint2 hi = *reinterpret_cast<const uint2*>(row + e);
+      const uint2 lo = *reinterpret_cast<const uint2*>(row + I + e);
+      const uint32_t hw[2] = {hi.x, hi.y}, lw[2] = {lo.x, lo.y};
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        v[st][2 * i] = __uint_as_float(hw[i] << 16) + __uint_as_float(lw[i] << 16);
+        v[st][2 * i + 1] = __uint_as_float(hw[i] & 0xffff0000u) + __uint_as_float(lw[i] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(v[st][i]));
+    }
+  }
+  bool bad = !(mx <= 3.4e38f);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    bad = bad || __shfl_xor((int)bad, o, 64);
+  }
+  int k = 0;
+  if (!bad && mx > 0.0f) {
+    int ex;
+    (void)frexpf(mx, &ex);  // mx < 2^ex
+    k = ldexpf(mx, 15 - ex) <= 32639.0f ? 15 - ex : 14 - ex;
+  }
+  uint8_t* out = reinterpret_cast<uint8_t*>(row);
+#pragma unroll
+  for (int st = 0; st < kSteps; ++st) {
+    const int e = 4 * (lane + 64 * st);
+    if (e < I) {
+      uint32_t w1 = 0, w2 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int H = bad ? 0 : (int)rintf(ldexpf(v[st][i], k));
+        const int p2 = ((H + 128) & 255) - 128;
+        w1 |= (uint32_t)(((H - p2) >> 8) & 255) << (8 * i);
+        w2 |= (uint32_t)(p2 & 255) << (8 * i);
+      }
+      const int c = e >> 6, o = e & 63;
+      *reinterpret_cast<uint32_t*>(out + c * 128 + o) = w1;
+      *reinterpret_cast<uint32_t*>(out + c * 128 + 64 + o) = w2;
+    }
+  }
+  if (lane == 0) hs[m] = bad ? __builtin_nanf("") : ldexpf(1.0f, -k);
 }
 
 // ---------------------------------------------------------------------------
@@ -1493,7 +1682,7 @@ namespace {
 template <int CH>
 hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint16_t* xb, const int32_t* offsets,
                          const int32_t* active, const int32_t* sorted_token, const int8_t* w13, const float* s13,
-                         const int8_t* w2, const float* s2, uint16_t* hb, uint16_t* yb, hipStream_t st) {
+                         const int8_t* w2, const float* s2, uint16_t* hb, uint16_t* yb, float* hs, hipStream_t st) {
   const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts, K = (int)d.top_k,
             I = (int)d.intermediate;
   const int M = T * K;
@@ -1607,38 +1796,49 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
     if (stages & kStageGateUp) {
       if (s64)
         hipLaunchKernelGGL((k_gemm<true, true, CH, 64>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
-                           offsets, sorted_token, w13, s13, hb, cap);
+                           offsets, sorted_token, w13, s13, hb, cap, nullptr);
       else if (ntb)
         hipLaunchKernelGGL((k_gemm<true, true, CH, 128>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
-                           offsets, sorted_token, w13, s13, hb, cap);
+                           offsets, sorted_token, w13, s13, hb, cap, nullptr);
       else if (ntb160)
         hipLaunchKernelGGL((k_gemm<true, true, CH, 160>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
-                           offsets, sorted_token, w13, s13, hb, cap);
+                           offsets, sorted_token, w13, s13, hb, cap, nullptr);
       else if (big)
         hipLaunchKernelGGL((k_gemm<true, false, CH, 160>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
-                           offsets, sorted_token, w13, s13, hb, cap);
+                           offsets, sorted_token, w13, s13, hb, cap, nullptr);
       else
         hipLaunchKernelGGL((k_gemm<true, false, CH, 128>), dim3(grid_for(I / 128)), dim3(256), 0, st, D, I, E, xb,
-                           offsets, sorted_token, w13, s13, hb, cap);
+                           offsets, sorted_token, w13, s13, hb, cap, nullptr);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
     }
     if (stages & kStageDown) {
+      if (CH == kChainF32 && hs != nullptr && down_planes_fits(d)) {
+        // h as two int8 planes with a per-row scale (in place), then the
+        // integer down product on 64-row tiles
+        hipLaunchKernelGGL(k_h_planes, dim3((M + 3) / 4), dim3(256), 0, st, M, I, hb, hs);
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        const int mt64 = (M + 63) / 64 + slots;
+        hipLaunchKernelGGL((k_gemm<false, false, kChainF32, 64, true>), dim3(((mt64 * (D / 256) + 7) / 8) * 8),
+                           dim3(256), 0, st, D, I, E, hb, offsets, sorted_token, w2, s2, yb, cap, hs);
+        return hipGetLastError();
+      }
       if (s64)
         hipLaunchKernelGGL((k_gemm<false, true, CH, 64>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
-                           offsets, sorted_token, w2, s2, yb, cap);
+                           offsets, sorted_token, w2, s2, yb, cap, nullptr);
       else if (ntb)
         hipLaunchKernelGGL((k_gemm<false, true, CH, 128>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
-                           offsets, sorted_token, w2, s2, yb, cap);
+                           offsets, sorted_token, w2, s2, yb, cap, nullptr);
       else if (ntb160)
         hipLaunchKernelGGL((k_gemm<false, true, CH, 160>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
-                           offsets, sorted_token, w2, s2, yb, cap);
+                           offsets, sorted_token, w2, s2, yb, cap, nullptr);
       else if (big)
         hipLaunchKernelGGL((k_gemm<false, false, CH, 160>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
-                           offsets, sorted_token, w2, s2, yb, cap);
+                           offsets, sorted_token, w2, s2, yb, cap, nullptr);
       else
         hipLaunchKernelGGL((k_gemm<false, false, CH, 128>), dim3(grid_for(D / 256)), dim3(256), 0, st, D, I, E, hb,
-                           offsets, sorted_token, w2, s2, yb, cap);
+                           offsets, sorted_token, w2, s2, yb, cap, nullptr);
       return hipGetLastError();
     }
     return hipSuccess;
@@ -1666,7 +1866,8 @@ hipError_t packed_stages(const kmoe_desc& d, int family, int stages, const uint1
 
 hipError_t launch_expert_packed(const kmoe_desc& d, int chain, int family, int stages, const void* x,
                                 const int32_t* offsets, const int32_t* active, const int32_t* sorted_token,
-                                const kmoe_packed_experts& p, void* h_sorted, void* y_sorted, hipStream_t st) {
+                                const kmoe_packed_experts& p, void* h_sorted, void* y_sorted, hipStream_t st,
+                                float* h_scale) {
   const uint16_t* xb = reinterpret_cast<const uint16_t*>(x);
   uint16_t* hb = reinterpret_cast<uint16_t*>(h_sorted);
   uint16_t* yb = reinterpret_cast<uint16_t*>(y_sorted);
@@ -1676,8 +1877,9 @@ hipError_t launch_expert_packed(const kmoe_desc& d, int chain, int family, int s
   const float* s2 = reinterpret_cast<const float*>(p.s2);
   if (chain == kChainF32)
     return packed_stages<kChainF32>(d, family, stages, xb, offsets, active, sorted_token, w13, s13, w2, s2, hb, yb,
-                                    st);
-  return packed_stages<kChainAct>(d, family, stages, xb, offsets, active, sorted_token, w13, s13, w2, s2, hb, yb, st);
+                                    h_scale, st);
+  return packed_stages<kChainAct>(d, family, stages, xb, offsets, active, sorted_token, w13, s13, w2, s2, hb, yb,
+                                  nullptr, st);
 }
 
 static WView make_view(const kmoe_weight& w) {

@@ -194,6 +194,7 @@ Workspace layout(const kmoe_desc& d, bool block) {
   // router's scratch (a bf16 router; the others need none)
   w.route_part = take(T <= (size_t)kSplitRouterMaxTokens ? 4 * route_split_part_floats(d)
                                                          : (T >= 2048 ? route_mfma_scratch_bytes(d) : 0));
+  w.h_scale = take(down_planes_fits(d) ? 4 * M : 0);
   w.normed = take(block ? act * T * D : 0);  // rms_norm(h) for kmoe_forward_block
   w.total = o;
   return w;
@@ -216,6 +217,13 @@ int family_of(const kmoe_desc& d) {
   if (d.tokens <= 16 * kmoe::kDecodeMaxRowBlocks) return kFamilyDecode;
   if (d.kernels == KMOE_KERNELS_DECODE && d.tokens <= kmoe::kRowsPathMaxTokens) return kFamilyRows;
   return kFamilyGemm;
+}
+
+bool down_planes_fits(const kmoe_desc& d) {
+  const int64_t M = d.tokens * d.top_k;
+  return enum_value(d.act_dtype) == KMOE_DTYPE_BF16 && chain_of(d) == kmoe::kChainF32 &&
+         family_of(d) == kFamilyGemm && M >= 96 * d.num_experts && d.hidden % 256 == 0 &&
+         d.intermediate % 128 == 0 && d.intermediate <= 64 * kmoe::kPlanesMaxChunks;
 }
 
 // Weights a layout-native expert stage reads.

@@ -42,6 +42,11 @@ constexpr int kDownCombineMaxAssignments = 32;  // T * K it takes
 //     two operands (hi + lo carries h to ~2^-17 relative).
 constexpr int kChainAct = 0;
 constexpr int kChainF32 = 1;
+// The whole-block call's large prefill chunks (down_planes_fits) feed the down
+// product h as two int8 digit planes of a 15-bit fixed-point value with one
+// power-of-two scale per row (k_h_planes), on the integer MFMA; rows up to
+// this many 64-wide chunks (I <= 2048).
+constexpr int kPlanesMaxChunks = 32;
 
 }  // namespace kmoe
 
@@ -140,8 +145,14 @@ bool packed_ok(const kmoe_desc& d, const kmoe_packed_experts* p);
 // that only kmoe_forward_block writes.
 struct Workspace {
   size_t topk_idx, topk_w, hist, group_sizes, offsets, active, sorted_token, sorted_expert, inv, h_sorted,
-      y_sorted, route_part, normed, total;
+      y_sorted, route_part, h_scale, normed, total;
 };
+// Whether the whole-block call's f32-chain down product takes h as int8 planes
+// (k_h_planes + the integer k_gemm): bf16 activations, the ragged program, at
+// least 96 rows per expert on average (where the grouped GEMMs run 64-row
+// planes tiles against 160-row bf16 ones), D % 256 == 0, I % 128 == 0,
+// I <= 2048. The workspace then holds one scale per row (Workspace::h_scale).
+bool down_planes_fits(const kmoe_desc& d);
 Workspace layout(const kmoe_desc& d, bool block);
 
 // --- argument checks ---------------------------------------------------------

@@ -58,10 +58,13 @@ hipError_t launch_dispatch(const kmoe_desc& d, const int32_t* topk_idx, const in
 // expert.hip
 // chain: kmoe::kChainAct or kmoe::kChainF32 (common.h); with kChainF32 and bf16
 // activations h_sorted holds [T*K][2I] bf16 (the hi and lo planes of h).
-// Packed int8 experts on MFMA.
+// Packed int8 experts on MFMA. With h_scale (M floats, the whole-block call
+// only) and down_planes_fits, the down stage first turns h_sorted's rows into
+// int8 planes in place (the caller's h_sorted is then no longer hi/lo planes).
 hipError_t launch_expert_packed(const kmoe_desc& d, int chain, int family, int stages, const void* x,
                                 const int32_t* offsets, const int32_t* active, const int32_t* sorted_token,
-                                const kmoe_packed_experts& p, void* h_sorted, void* y_sorted, hipStream_t st);
+                                const kmoe_packed_experts& p, void* h_sorted, void* y_sorted, hipStream_t st,
+                                float* h_scale = nullptr);
 // Layout-native experts (any weight kind), one sequential fmaf chain per output.
 hipError_t launch_expert_generic(const kmoe_desc& d, int chain, int stages, const void* x, const int32_t* sorted_token,
                                  const int32_t* sorted_expert, const kmoe_weight* gate, const kmoe_weight* up,

@@ -209,6 +209,16 @@ static void stage_cases() {
   CHECK(route_mfma_preferred(l30, RB) && !route_mfma_preferred(desc(1024, 2048, 128, 8), RB));
   CHECK(route_mfma_preferred(desc(2048, 4096, 128, 8, 1536), RB) && route_mfma_preferred(desc(4096, 4096, 128, 8, 1536), RB));
   CHECK(!route_mfma_preferred(desc(2047, 4096, 128, 8, 1536), RB) && !route_mfma_preferred(desc(4096, 4096, 128, 8, 1536, KMOE_DTYPE_F32), RB));
+  // the int8-plane down product: the ragged program on bf16 activations from 96 rows per expert
+  CHECK(down_planes_fits(desc(1536, 2048, 128, 8, 768)) && !down_planes_fits(desc(1535, 2048, 128, 8, 768)));
+  CHECK(!down_planes_fits(desc(4096, 2048, 128, 8, 768, KMOE_DTYPE_F32)) &&
+        !down_planes_fits(desc(4096, 2048, 128, 8, 768, KMOE_DTYPE_BF16, 0, 0, KMOE_IMPL_GATHER_EINSUM)));
+  CHECK(!down_planes_fits(desc(4096, 2048, 128, 8, 768, KMOE_DTYPE_BF16, 4096)) &&  // threshold: gather program
+        !down_planes_fits(desc(4096, 2048, 128, 8, 4096)) && down_planes_fits(desc(2048, 4096, 128, 8, 1536)));
+  {
+    const Workspace wp = layout(desc(2048, 2048, 128, 8, 768), false), wn = layout(desc(1024, 2048, 128, 8, 768), false);
+    CHECK(wp.normed - wp.h_scale == (size_t)4 * 2048 * 8 && wn.normed == wn.h_scale);
+  }
   EXPECT(validate_dispatch(&d, I, I, I, I, I, I, I, nullptr), KMOE_ERR_INVALID_ARG, "kmoe_dispatch");
   EXPECT(validate_dispatch(&d, I, I, I, I, I, I, I, I), KMOE_OK, nullptr);
   EXPECT(validate_combine(&d, P, nullptr, Fp, P), KMOE_ERR_INVALID_ARG, "kmoe_combine");

@@ -416,6 +416,41 @@ def test_whole_block_matches_staged_path(dev, l30, l30t, T, impl):
             assert torch.equal(out.reshape(T, layer.D), staged.reshape(T, layer.D))
 
 
+@pytest.mark.parametrize("impl", ["ragged", "gather_einsum"])
+def test_large_chunks_feed_h_as_int8_planes(dev, l30, l30t, impl):
+    """From 96 rows per expert on average (30B-A3B: 1536 tokens) the whole-block
+    call's f32-chain down product takes h as two int8 planes with a per-row scale
+    (15 bits relative to the row's largest |h|) instead of bf16 hi and lo planes;
+    the staged calls keep hi and lo. So the ragged program's outputs differ from
+    the staged ones by the feed's rounding alone: a few 1e-4 mean-rel, inside the
+    1e-3 bar, and not bit for bit (the planes path ran). The gather program's
+    x.dtype chain has no f32 h: bit-identical."""
+    from kappa_amd.qwen3 import moe_stages
+    from kappa_amd.qwen3.ffn_moe import PACK_CACHE, _moe_forward
+
+    layer = l30 if impl == "ragged" else l30t
+    T = 2048
+    x = make_x(T, layer.D, seed=1700)
+    r, d = _route_and_dispatch(x, layer.router, layer.E, layer.K)
+    h, y = moe_stages.expert_ffn(x, d, layer.gate, layer.up, layer.down, k=layer.K, impl=impl)
+    staged = moe_stages.combine(y, d["inv"], r["w"], k=layer.K, impl=impl).reshape(T, layer.D)
+    packed = PACK_CACHE.get(layer.gate, layer.up, layer.down)
+    out, idx, w = _moe_forward(
+        x.reshape(1, T, layer.D), layer.router, layer.gate, layer.up, layer.down, num_experts=layer.E,
+        num_experts_per_tok=layer.K, packed=packed, return_routing=True, **forward_args(impl),
+    )  # fmt: skip
+    out = out.reshape(T, layer.D)
+    assert torch.equal(idx, r["idx"])
+    if impl == "gather_einsum":
+        assert torch.equal(out, staged)
+        return
+    a, b = bf16_np(out), bf16_np(staged)
+    rel, mabs = mean_rel(a, b), float(np.abs(a - b).max())
+    print(f"planes vs hi/lo: max-abs {mabs:.2e} mean-rel {rel:.2e}")
+    assert not torch.equal(out, staged)
+    assert 1e-5 < rel <= 5e-4 and mabs <= 2e-2
+
+
 @pytest.mark.parametrize("T", [4, 64, 512])
 def test_packed_experts_alone(dev, l30, T):
     """A model that prepacked at load time passes packed= and no source weights; the

@@ -1,0 +1,96 @@
+"""How the ragged program's h reaches the down product, and what each form costs (CPU).
+
+In the reference, the ragged program's h is float32 and meets float32 weights,
+`q * s` (kappa/qwen3/ffn_moe.py:203-213). The kernels feed the matrix cores
+either h's bf16 hi and lo planes (hi = bf16(h), lo = bf16(h - hi)), both
+multiplied by the exact integer weights (two bf16 passes), or, in the
+whole-block call's large prefill chunks (96 rows per expert and more), two
+int8 digit planes of h rounded to 15 bits relative to the row's largest |h|
+(k_h_planes), multiplied by the raw int8 weights on the integer MFMA (the work
+of one bf16 pass, no weight conversion). This test measures, on the golden
+r30_w8c case (the 30B-A3B per-token shape, D = 2048, I = 768, top-8,
+per-channel W8), how far the layer output moves from the golden when the
+golden's own float32 h reaches the down product in each form, everything else
+(the f32 sums, y rounded to bf16, the bf16 running-add combine in j order) as
+the golden program computes it:
+
+- hi + lo planes and three int8 planes: within 2e-5 mean-rel of the golden;
+- two int8 planes (the large-chunk feed): within 2.5e-4, a quarter of the
+  1e-3 bar;
+- one fp16 plane: further (about 4.8e-4), for comparison.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+from inputs import GOLDEN_SPECS, bf16_rne, make_inputs  # noqa: E402
+
+
+def _planes(h: np.ndarray, n: int) -> np.ndarray:
+    """h rounded to n signed int8 planes with one power-of-two scale per row
+    (|H| <= 127 * (256^n - 1) / 255, so every plane digit fits int8)."""
+    cap = 127.0 * (256.0**n - 1.0) / 255.0
+    m = np.abs(h).max(axis=1, keepdims=True).astype(np.float64)
+    m = np.where(m > 0, m, 1.0)
+    scale = 2.0 ** np.floor(np.log2(cap / m))
+    H = np.rint(h.astype(np.float64) * scale)
+    assert np.abs(H).max() <= cap
+    return H / scale
+
+
+FEEDS = {
+    "f32": lambda h: h.astype(np.float64),
+    "hi_lo": lambda h: bf16_rne(h).astype(np.float64) + bf16_rne(h - bf16_rne(h)).astype(np.float64),
+    "fp16": lambda h: h.astype(np.float16).astype(np.float64),
+    "int8_x2": lambda h: _planes(h, 2),
+    "int8_x3": lambda h: _planes(h, 3),
+}
+
+
+@pytest.fixture(scope="module")
+def golden():
+    spec = next(s for s in GOLDEN_SPECS if s.name == "r30_w8c")
+    g = dict(np.load(os.path.join(ROOT, "tests", "golden", "r30_w8c.npz")))
+    return spec, make_inputs(spec), g
+
+
+def _out(spec, inp, g, feed) -> np.ndarray:
+    q, s = inp["down"]
+    wd = (q.astype(np.float32) * s).astype(np.float64)  # to_compute_dtype(down, f32)
+    T, K = g["idx"].shape
+    sorted_e = g["idx"].reshape(-1)[g["order"]]
+    hf = FEEDS[feed](g["h_sorted"])
+    y_sorted = np.empty((T * K, spec.D), np.float32)
+    for m in range(T * K):
+        y_sorted[m] = (hf[m] @ wd[sorted_e[m]]).astype(np.float32)
+    y = bf16_rne(y_sorted[g["inv"]]).reshape(T, K, -1)
+    out = np.zeros((T, spec.D), np.float32)
+    for j in range(K):
+        out = bf16_rne(out + bf16_rne(y[:, j] * g["w"][:, j : j + 1]))
+    return out
+
+
+def _mean_rel(a, b):
+    return float(np.abs(a - b).mean() / np.abs(b).mean())
+
+
+def test_h_feeds_against_the_golden(golden):
+    spec, inp, g = golden
+    rel = {f: _mean_rel(_out(spec, inp, g, f), g["out"]) for f in FEEDS}
+    print(" ".join(f"{f} {v:.2e}" for f, v in rel.items()))
+    # the restatement reproduces the golden from its own h
+    assert rel["f32"] <= 1e-6
+    # the decode and stage kernels' feed, and three int8 planes: as close as the f32 h
+    assert rel["hi_lo"] <= 2e-5 and rel["int8_x3"] <= 2e-5
+    # the large prefill chunks' feed: a quarter of the bar
+    assert 1e-5 < rel["int8_x2"] <= 2.5e-4
+    # one fp16 plane, for comparison: further than two int8 planes
+    assert rel["fp16"] > rel["int8_x2"]
