@@ -1277,25 +1277,25 @@ __global__ __launch_bounds__(256) void k_h_planes(int M, int I, uint16_t* __rest
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= M) return;
   uint16_t* row = h + (size_t)m * 2 * I;
-  // lane L, step s: the four elements from 4 (L + 64 s) on (8-byte loads of
-  // each bf16 plane, 4-byte stores of each int8 plane)
-  constexpr int kSteps = kPlanesMaxChunks / 4;
-  float v[kSteps][4];
+  // lane L, step s: the eight elements from 8 (L + 64 s) on (16-byte loads of
+  // each bf16 plane, 8-byte stores of each int8 plane)
+  constexpr int kSteps = kPlanesMaxChunks / 8;
+  float v[kSteps][8];
   float mx = 0.0f;
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) {
-    const int e = 4 * (lane + 64 * st);
+    const int e = 8 * (lane + 64 * st);
     if (e < I) {
-      const uint2 hi = *reinterpret_cast<const uint2*>(row + e);
-      const uint2 lo = *reinterpret_cast<const uint2*>(row + I + e);
-      const uint32_t hw[2] = {hi.x, hi.y}, lw[2] = {lo.x, lo.y};
+      const uint4 hi = *reinterpret_cast<const uint4*>(row + e);
+      const uint4 lo = *reinterpret_cast<const uint4*>(row + I + e);
+      const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w}, lw[4] = {lo.x, lo.y, lo.z, lo.w};
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < 4; ++i) {
         v[st][2 * i] = __uint_as_float(hw[i] << 16) + __uint_as_float(lw[i] << 16);
         v[st][2 * i + 1] = __uint_as_float(hw[i] & 0xffff0000u) + __uint_as_float(lw[i] & 0xffff0000u);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, fabsf(v[st][i]));
+      for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[st][i]));
     }
   }
   bool bad = !(mx <= 3.4e38f);
@@ -1313,19 +1313,19 @@ __global__ __launch_bounds__(256) void k_h_planes(int M, int I, uint16_t* __rest
   uint8_t* out = reinterpret_cast<uint8_t*>(row);
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) {
-    const int e = 4 * (lane + 64 * st);
+    const int e = 8 * (lane + 64 * st);
     if (e < I) {
-      uint32_t w1 = 0, w2 = 0;
+      uint32_t w1[2] = {0, 0}, w2[2] = {0, 0};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 8; ++i) {
         const int H = bad ? 0 : (int)rintf(ldexpf(v[st][i], k));
         const int p2 = ((H + 128) & 255) - 128;
-        w1 |= (uint32_t)(((H - p2) >> 8) & 255) << (8 * i);
-        w2 |= (uint32_t)(p2 & 255) << (8 * i);
+        w1[i >> 2] |= (uint32_t)(((H - p2) >> 8) & 255) << (8 * (i & 3));
+        w2[i >> 2] |= (uint32_t)(p2 & 255) << (8 * (i & 3));
       }
       const int c = e >> 6, o = e & 63;
-      *reinterpret_cast<uint32_t*>(out + c * 128 + o) = w1;
-      *reinterpret_cast<uint32_t*>(out + c * 128 + 64 + o) = w2;
+      *reinterpret_cast<uint2*>(out + c * 128 + o) = uint2{w1[0], w1[1]};
+      *reinterpret_cast<uint2*>(out + c * 128 + 64 + o) = uint2{w2[0], w2[1]};
     }
   }
   if (lane == 0) hs[m] = bad ? __builtin_nanf("") : ldexpf(1.0f, -k);
