@@ -150,8 +150,10 @@ struct Workspace {
 // Whether the whole-block call's f32-chain down product takes h as int8 planes
 // (k_h_planes + the integer k_gemm): bf16 activations, the ragged program, at
 // least 96 rows per expert on average (where the grouped GEMMs run 64-row
-// planes tiles against 160-row bf16 ones), D % 256 == 0, I % 128 == 0,
-// I <= 2048. The workspace then holds one scale per row (Workspace::h_scale).
+// planes tiles against 160-row bf16 ones; below, at T = 256 to 1280, the
+// planes measured even with the bf16 hi/lo tiles), D % 256 == 0,
+// I % 128 == 0, I <= 2048. The workspace then holds one scale per row
+// (Workspace::h_scale).
 bool down_planes_fits(const kmoe_desc& d);
 Workspace layout(const kmoe_desc& d, bool block);
 
