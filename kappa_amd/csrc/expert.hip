@@ -874,22 +874,24 @@ __device__ __forceinline__ int a_swz(int r, int p) { return r * 64 + (a_piece(r,
 constexpr int kGemmRows = 128;                // rows per tile (the 128-row form)
 constexpr int kGemmB = 16 * 1024;             // B stage: 16 cells x 64 k x 16 columns int8
 constexpr int kGemmBJ = 4;                    // B loads per wave per chunk (one cell each)
-// weight ring depth of the int8-plane down product: two chunks (48 KB, three
-// blocks per CU); three (64 KB, two blocks) ran 30B-A3B T = 4096 476 -> 492 us
-// and 235B-A22B T = 2048 813 -> 823 us per layer
+// ring depths of the int8-plane down product (A and weights alike): two chunks
+// (48 KB, three blocks per CU). Three, both issued two chunks ahead (72 KB, two
+// blocks per CU), ran 30B-A3B T = 2048 / 4096 296 / 470 -> 301 / 480 us and
+// 235B-A22B T = 2048 791 -> 803 us per layer; a three-deep weight ring with the
+// activation rows one chunk ahead, 476 -> 492 us at T = 4096.
 constexpr int kI8Ring = 2;
 
 // Tile shapes: 128 rows with a weight ring three chunks deep (80 KB), or 160
 // rows with a ring two chunks deep (72 KB; an expert with up to 160 rows is
 // one tile): either way two blocks fill a CU's LDS. 64 rows with a ring two
 // chunks deep (48 KB): three blocks per CU.
-template <int RW, int NB = 0>
+template <int RW, int NB = 0, int NA = 2>
 struct GemmShape {
   static_assert(RW == 64 || RW == 128 || RW == 160, "tile rows");
   static constexpr int kRows = RW;
   static constexpr int kA = RW * 128;          // A stage: RW rows x 64 bf16
   static constexpr int kAJ = RW / 32;          // A loads per wave per chunk (8 rows each)
-  static constexpr int kNA = 2;                // A ring depth
+  static constexpr int kNA = NA;               // A ring depth
   static constexpr int kNB = NB ? NB : (RW == 128 ? 3 : 2);  // B ring depth
   static constexpr int kLds = kNA * kA + kNB * kGemmB;
 };
@@ -1043,8 +1045,9 @@ template <int MT, bool NTB, int RW>
 __device__ __forceinline__ void gemm_tile_i8(uint8_t* smem, const GemmLoads<GemmShape<RW>::kAJ>& gl, int KC, int wv,
                                              int rows, int row0, int nt, const uint16_t* __restrict__ src,
                                              const float* __restrict__ hs, uint16_t* __restrict__ dst, int Ndim) {
-  using Sh = GemmShape<RW, kI8Ring>;
+  using Sh = GemmShape<RW, kI8Ring, kI8Ring>;
   constexpr int kGemmA = Sh::kA, kGemmAJ = Sh::kAJ, kGemmNA = Sh::kNA, kGemmNB = Sh::kNB;
+  static_assert(kGemmNA == kGemmNB && (kGemmNA == 2 || kGemmNA == 3), "rings of two or three chunks");
   const int lane = threadIdx.x & 63;
   const uint32_t lds0 = lds_addr(smem);
   const uint8_t* const bring = smem + kGemmNA * kGemmA;
@@ -1056,44 +1059,45 @@ __device__ __forceinline__ void gemm_tile_i8(uint8_t* smem, const GemmLoads<Gemm
       a1c[mi][g] = int32x4{0, 0, 0, 0};
       a2c[mi][g] = int32x4{0, 0, 0, 0};
     }
-  auto issue_a = [&](int c) {
-    const uint32_t st = lds0 + (uint32_t)((c & 1) * kGemmA + wv * kGemmAJ * 1024);
+  // chunk c's A and weights both in stage c % depth
+  auto issue = [&](int c) {
+    const uint32_t sa = lds0 + (uint32_t)((c % kGemmNA) * kGemmA + wv * kGemmAJ * 1024);
     const uint16_t* abase = src + c * 64;
 #pragma unroll
-    for (int j = 0; j < kGemmAJ; ++j) dma16(gl.avoff[j], abase, st + j * 1024);
-  };
-  auto issue_b = [&](int b) {
-    const uint32_t st = lds0 + (uint32_t)(kGemmNA * kGemmA + (b % kGemmNB) * kGemmB + wv * 4096);
+    for (int j = 0; j < kGemmAJ; ++j) dma16(gl.avoff[j], abase, sa + j * 1024);
+    const uint32_t sb = lds0 + (uint32_t)(kGemmNA * kGemmA + (c % kGemmNB) * kGemmB + wv * 4096);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       if (NTB)
-        dma16_stream(lane * 16, gl.bsrc[g] + b * 1024, st + g * 1024);
+        dma16_stream(lane * 16, gl.bsrc[g] + c * 1024, sb + g * 1024);
       else
-        dma16(lane * 16, gl.bsrc[g] + b * 1024, st + g * 1024);
+        dma16(lane * 16, gl.bsrc[g] + c * 1024, sb + g * 1024);
     }
   };
-  // the PL = 1 schedule of gemm_tile: kAhead weight chunks issued ahead
-  constexpr int kAhead = kGemmNB == 3 ? 2 : 1;
-  issue_b(0);
-  issue_a(0);
-  if (kAhead == 2 && 1 < KC) {
-    issue_b(1);
-    vm_barrier<kGemmBJ>();
-  } else {
+  // chunks issued ahead: depth - 1. Iteration c issues chunk c + depth - 1 (into
+  // the stage chunk c - 1 used, free after the previous iteration's barrier)
+  // and at its end waits for chunk c + 1: the only loads left outstanding are
+  // those of the chunks issued after it, kGemmAJ + 4 each.
+  constexpr int kAhead = kGemmNA - 1;
+  constexpr int kPer = kGemmAJ + kGemmBJ;
+#pragma unroll
+  for (int c = 0; c < kAhead + 1; ++c)
+    if (c < KC) issue(c);
+  // chunk 0 before the first iteration: the chunks issued after it may stay outstanding
+  const int after0 = min(KC - 1, kAhead);
+  if (after0 == 2)
+    vm_barrier<2 * kPer>();
+  else if (after0 == 1)
+    vm_barrier<kPer>();
+  else
     vm_barrier<0>();
-  }
   for (int c = 0; c < KC; ++c) {
-    bool b_ahead = false;
-    if (c + 1 < KC) issue_a(c + 1);
-    if (c + kAhead < KC) {
-      issue_b(c + kAhead);
-      b_ahead = kAhead == 2;
-    }
+    if (c + kAhead < KC && c > 0) issue(c + kAhead);
     int32x4 q[4];
     const uint8_t* bp = bring + (c % kGemmNB) * kGemmB + wv * 4096 + lane * 16;
 #pragma unroll
     for (int g = 0; g < 4; ++g) q[g] = *reinterpret_cast<const int32x4*>(bp + g * 1024);
-    const uint16_t* As = reinterpret_cast<const uint16_t*>(smem + (c & 1) * kGemmA);
+    const uint16_t* As = reinterpret_cast<const uint16_t*>(smem + (c % kGemmNA) * kGemmA);
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi) {
       const int r = mi * 16 + (lane & 15);
@@ -1106,8 +1110,10 @@ __device__ __forceinline__ void gemm_tile_i8(uint8_t* smem, const GemmLoads<Gemm
       }
     }
     if (c + 1 < KC) {
-      if (b_ahead)
-        vm_barrier<kGemmBJ>();
+      // outstanding after chunk c + 1: the chunks issued after it
+      const int after = min(KC - 1, c + kAhead) - (c + 1);
+      if (kAhead == 2 && after > 0)
+        vm_barrier<kPer>();
       else
         vm_barrier<0>();
     }
@@ -1142,7 +1148,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
                                                   const int8_t* __restrict__ wp, const float* __restrict__ sp,
                                                   uint16_t* __restrict__ dst, int cap, const float* __restrict__ hs) {
   static_assert(!I8 || (!GATEUP && CH == kChainF32 && RW == 64), "int8 planes: the f32 chain's down product");
-  using Sh = GemmShape<RW, I8 ? kI8Ring : 0>;
+  using Sh = GemmShape<RW, I8 ? kI8Ring : 0, I8 ? kI8Ring : 2>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Sh::kLds];
   // set-up scratch inside the ring (no loads are in flight yet)
   int* const mtp = reinterpret_cast<int*>(smem);
