@@ -94,3 +94,49 @@ def test_h_feeds_against_the_golden(golden):
     assert 1e-5 < rel["int8_x2"] <= 2.5e-4
     # one fp16 plane, for comparison: further than two int8 planes
     assert rel["fp16"] > rel["int8_x2"]
+
+
+def _kernel_planes(h: np.ndarray):
+    """k_h_planes' arithmetic for one row (kappa_amd/csrc/expert.hip): k from the
+    row's largest |h| (frexp exponent ex, k = 15 - ex, or 14 - ex when that
+    would pass 32639), H = rint(h * 2^k) in f32, the digits p2 = ((H + 128) & 255)
+    - 128 and p1 = (H - p2) >> 8."""
+    h = h.astype(np.float32)
+    mx = np.float32(np.abs(h).max())
+    k = 0
+    if mx > 0:
+        _, ex = np.frexp(mx)
+        k = 15 - int(ex) if np.ldexp(mx, 15 - int(ex)) <= 32639.0 else 14 - int(ex)
+    H = np.rint(np.ldexp(h, k).astype(np.float32)).astype(np.int64)
+    p2 = ((H + 128) & 255) - 128
+    p1 = (H - p2) >> 8
+    return k, H, p1, p2
+
+
+def test_plane_digits_fit_int8_and_bound_the_error():
+    """Across magnitudes from subnormal to 1e30, rows with a value exactly at a
+    power of two or just under the 32639 boundary, and all-zero rows: the two
+    digits fit int8 ([-127, 127] and [-128, 127]), 256 p1 + p2 is H, and H 2^-k
+    is within half a grid step of every element: the largest |H| is above
+    16319, so a step is at most 2^-14 of the row's largest |h|."""
+    rng = np.random.default_rng(7)
+    rows = [rng.standard_normal(768).astype(np.float32) * np.float32(s) for s in (1e-40, 1e-20, 1e-3, 1.0, 7.9, 1e10, 1e30)]
+    edge = rng.standard_normal(768).astype(np.float32)
+    edge[5] = np.float32(32639.0 / 2**15)  # max |h| * 2^15 exactly at the boundary
+    rows += [edge, np.zeros(768, np.float32), np.full(768, 2.0, np.float32), np.full(768, -0.75, np.float32)]
+    heavy = rng.standard_normal(768).astype(np.float32)
+    heavy[:4] *= 300.0  # a few outliers
+    rows.append(heavy)
+    for h in rows:
+        k, H, p1, p2 = _kernel_planes(h)
+        assert np.all((p1 >= -127) & (p1 <= 127)) and np.all((p2 >= -128) & (p2 <= 127))
+        assert np.array_equal(256 * p1 + p2, H) and np.abs(H).max() <= 32639
+        mx = float(np.abs(h).max())
+        if mx == 0:
+            assert not H.any()
+            continue
+        err = np.abs(np.ldexp(H.astype(np.float64), -k) - h.astype(np.float64)).max()
+        # half a grid step, plus the f32 rounding of tiny rows' subnormal scaling
+        assert err <= 2.0**-15 * mx * 1.0001 + 1e-45, (mx, err)
+        # the grid uses at least half its range
+        assert np.abs(H).max() > 16319
