@@ -451,6 +451,30 @@ def test_large_chunks_feed_h_as_int8_planes(dev, l30, l30t, impl):
     assert 1e-5 < rel <= 5e-4 and mabs <= 2e-2
 
 
+def test_large_chunk_nonfinite_row_stays_in_its_token(dev, l30):
+    """In the int8-plane down product every h row has its own scale: a token
+    whose h overflows f32 (x of 3e38) gets a non-finite output row, and every
+    other token's output stays finite and equal, to rounding, to the same call
+    with that token replaced by an ordinary row."""
+    from kappa_amd.qwen3.ffn_moe import _moe_forward
+
+    T, bad = 2048, 7
+    x = make_x(T, l30.D, seed=1800)
+    clean = x.clone()
+    x[bad] = 3e38
+    outs = []
+    for xi in (x, clean):
+        o = _moe_forward(
+            xi.reshape(1, T, l30.D), l30.router, l30.gate, l30.up, l30.down, num_experts=l30.E,
+            num_experts_per_tok=l30.K, packed=None, **forward_args("ragged"),
+        )  # fmt: skip
+        outs.append(bf16_np(o.reshape(T, l30.D)))
+    keep = np.arange(T) != bad
+    assert not np.isfinite(outs[0][bad]).all()
+    assert np.isfinite(outs[0][keep]).all()
+    assert mean_rel(outs[0][keep], outs[1][keep]) <= 1e-5
+
+
 @pytest.mark.parametrize("T", [4, 64, 512])
 def test_packed_experts_alone(dev, l30, T):
     """A model that prepacked at load time passes packed= and no source weights; the
