@@ -167,7 +167,11 @@ kmoe_status kmoe_prepack_bytes(const kmoe_desc* desc, kmoe_packed_sizes* sizes);
  * `packed` may be NULL: int8 experts then run on the layout-native kernels.
  * topk_idx_out [T,K] int32 and topk_w_out [T,K] (x dtype) are optional.
  * GATHER_EINSUM with per-channel scales and more than one expert is
- * KMOE_ERR_INVALID_ARG: the reference's gather program cannot apply them. */
+ * KMOE_ERR_INVALID_ARG: the reference's gather program cannot apply them.
+ * The RAGGED program with bf16 activations and packed experts feeds its down
+ * product h as two int8 planes with one power-of-two scale per row (15 bits
+ * of the row's largest |h|) from 96 rows per expert on average (T*K >= 96 E),
+ * and as bf16 hi and lo planes below (see kmoe_expert_ffn). */
 kmoe_status kmoe_forward(const kmoe_desc* desc, const void* x, const kmoe_weight* router, const kmoe_weight* gate,
                          const kmoe_weight* up, const kmoe_weight* down, const kmoe_packed_experts* packed, void* out,
                          int32_t* topk_idx_out, void* topk_w_out, void* workspace, size_t workspace_bytes,
