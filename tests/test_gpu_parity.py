@@ -266,13 +266,15 @@ def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48, impl="ragged
     return od
 
 
-@pytest.mark.parametrize("T", [240, 512, 704, 1024, 1280, 2048, 4096])
+@pytest.mark.parametrize("T", [240, 512, 704, 1024, 1280, 1535, 1536, 2048, 4096])
 def test_30b_prefill_ragged(dev, l30, T):
     """The prefill chunks under the reference's ragged program (ragged_jax with its
     default threshold of 64: these sizes run _moe_ragged). Every grouped-GEMM tile
     form is reached: 64-row tiles (T=240, 512, 704), 128-row tiles with
     nontemporal weights (T=1024, 64 rows per expert) and without (T=1280, 80),
-    160-row tiles with (T=2048) and without (T=4096)."""
+    160-row tiles with (T=2048) and without (T=4096). From T=1536 (96 rows per
+    expert) the down product takes h as int8 planes; T=1535 is the last size
+    with the bf16 hi and lo planes."""
     from kappa_amd.qwen3 import moe_layer_config
 
     cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_impl="ragged_jax")
