@@ -845,10 +845,17 @@ def test_two_phase_router_30b(dev, l30, T):
     _route_two_phase_check(x, skew_router(l30.router, lam=1.5), l30.E, l30.K)
 
 
-@pytest.mark.parametrize("D,E,K,T", [(4096, 128, 8, 300), (4096, 128, 8, 2048), (1024, 64, 4, 333), (512, 256, 8, 700)])
+@pytest.mark.parametrize(
+    "D,E,K,T",
+    [(4096, 128, 8, 300), (4096, 128, 8, 2048), (1024, 64, 4, 333), (512, 256, 8, 700), (2048, 48, 6, 500),
+     (1024, 16, 2, 400), (512, 240, 8, 333)],
+)  # fmt: skip
 def test_two_phase_router_shapes(dev, D, E, K, T):
     """The 235B-A22B router (64 slices per candidate) and other slice counts and
-    expert counts (the kernel's template forms)."""
+    expert counts (the kernel's template forms), including expert counts whose
+    16-expert tiles do not divide the block's waves (48: five reduction splits
+    of three tiles, one wave idle in phase 1; 240: fifteen tiles, one wave
+    idle) and a single tile (16 experts, sixteen reduction splits)."""
     g = torch.Generator(device="cuda").manual_seed(D + E + T)
     router = (torch.randn(D, E, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
     x = make_x(T, D, seed=1300 + T)
