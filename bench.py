@@ -808,8 +808,8 @@ def main():
             result["prefill"]["library_reference"] = library_reference(4096, D, I, E, K)
 
     if not args.quick:
-        # routing near ties against another summation order, per BASELINE config
-        # (the inputs of the timed points above)
+        # routing near ties against another summation order, per measured
+        # workload (the inputs of the timed points above)
         from inputs import GOLDEN_SPECS, make_inputs
 
         margins = {}
