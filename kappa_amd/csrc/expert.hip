@@ -104,20 +104,29 @@ __device__ __forceinline__ floatx4 mfma16(const bf16x8 a, const bf16x8 b, const 
 
 // Block-wide tile prefix over experts: mtp[e] = sum_{e' < e} ceil(min(group_size[e'], cap) / BM), mtp[E] = total.
 // The first 256 threads compute it (E <= 1024); blockDim.x must be a multiple of 64, at least 256.
-// wsum: 4 ints of LDS scratch.
+// wsum: 4 ints of LDS scratch. offs (optional, E + 1 ints of LDS): a copy of offsets, so
+// the caller's later lookups of its expert's row range are LDS reads, not another global
+// round trip.
 template <int BM>
-__device__ void tile_prefix(const int32_t* __restrict__ offsets, int E, int cap, int* mtp, int* wsum) {
+__device__ void tile_prefix(const int32_t* __restrict__ offsets, int E, int cap, int* mtp, int* wsum,
+                            int* offs = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   int c[4];
   int local = 0, incl = 0;
   if (tid < 256) {
+    // offsets[4 tid .. 4 tid + 4], clamped to the array: five loads in flight
+    // together (guarded loads would each wait a round trip of their own)
+    int o[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) o[i] = offsets[min(tid * 4 + i, E)];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid * 4 + i;
-      c[i] = 0;
-      if (e < E) c[i] = (min(offsets[e + 1] - offsets[e], cap) + BM - 1) / BM;
+      c[i] = e < E ? (min(o[i + 1] - o[i], cap) + BM - 1) / BM : 0;
+      if (offs != nullptr && e <= E) offs[e] = o[i];
       local += c[i];
     }
+    if (offs != nullptr && tid * 4 + 4 == E) offs[E] = o[4];
     incl = local;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -988,8 +997,10 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads<GemmSha
 #pragma unroll
       for (int mi = 0; mi < MT; ++mi) {
         const bf16x8 a = *reinterpret_cast<const bf16x8*>(As + a_swz(mi * 16 + (lane & 15), p));
+        // weights as the first operand: the accumulator tile is the output
+        // transposed, so a lane holds four consecutive columns of one row
 #pragma unroll
-        for (int g = 0; g < 4; ++g) acc[mi][g] = mfma16(a, st ? hi[g] : lo[g], acc[mi][g]);
+        for (int g = 0; g < 4; ++g) acc[mi][g] = mfma16(st ? hi[g] : lo[g], a, acc[mi][g]);
       }
     }
     if (c + 1 < KC) {
@@ -1000,33 +1011,53 @@ __device__ __forceinline__ void gemm_tile(uint8_t* smem, const GemmLoads<GemmSha
     }
   }
 
-  // epilogue: lane holds rows 4*(lane/16)+j of each 16x16 tile, column lane%16
+  // epilogue: lane holds row mi*16 + lane%16 and columns 4*(lane/16) + j of
+  // cell g, stored as 8-byte runs. kChainF32 scales each column: lane c holds
+  // column c's scale, shuffled to the lanes that hold the column (every lane
+  // takes part, before the lanes past the tile's rows drop out).
+  float scq[4][4];
+  if (CH == kChainF32) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) scq[g][j] = __shfl(gl.sc[g], 4 * (lane >> 4) + j, 64);
+  }
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi) {
+    const int row = mi * 16 + (lane & 15);
+    if (row >= rows) continue;
+    uint16_t* drow = dst + (size_t)(row0 + row) * (GATEUP && CH == kChainF32 ? 2 * Ndim : Ndim);
+    if (GATEUP) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = mi * 16 + 4 * (lane >> 4) + j;
-      if (row >= rows) continue;
-      uint16_t* drow = dst + (size_t)(row0 + row) * (GATEUP && CH == kChainF32 ? 2 * Ndim : Ndim);
-      if (GATEUP) {
+      for (int g = 0; g < 2; ++g) {
+        const int col = nt * 128 + wv * 32 + g * 16 + 4 * (lane >> 4);
+        float hv[4], lv[4];
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const int col = nt * 128 + wv * 32 + g * 16 + (lane & 15);
+        for (int j = 0; j < 4; ++j) {
           if (CH == kChainAct) {
             const float gv = round_bf16(acc[mi][g][j]);
             const float uv = round_bf16(acc[mi][g + 2][j]);
-            drow[col] = f32_to_bf16_bits(swiglu<true>(gv, uv));
+            hv[j] = swiglu<true>(gv, uv);
           } else {
-            const float gv = __fmul_rn(acc[mi][g][j], gl.sc[g]);
-            const float uv = __fmul_rn(acc[mi][g + 2][j], gl.sc[g + 2]);
-            split_bf16(swiglu<false>(gv, uv), drow[col], drow[Ndim + col]);
+            const float gv = __fmul_rn(acc[mi][g][j], scq[g][j]);
+            const float uv = __fmul_rn(acc[mi][g + 2][j], scq[g + 2][j]);
+            const float h = swiglu<false>(gv, uv);
+            hv[j] = round_bf16(h);
+            lv[j] = __fsub_rn(h, hv[j]);
           }
         }
-      } else {
+        *reinterpret_cast<uint2*>(drow + col) = uint2{pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3])};
+        if (CH == kChainF32)
+          *reinterpret_cast<uint2*>(drow + Ndim + col) = uint2{pack_bf16x2(lv[0], lv[1]), pack_bf16x2(lv[2], lv[3])};
+      }
+    } else {
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-          drow[nt * 256 + wv * 64 + g * 16 + (lane & 15)] =
-              f32_to_bf16_bits(CH == kChainF32 ? __fmul_rn(acc[mi][g][j], gl.sc[g]) : acc[mi][g][j]);
+      for (int g = 0; g < 4; ++g) {
+        float o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = CH == kChainF32 ? __fmul_rn(acc[mi][g][j], scq[g][j]) : acc[mi][g][j];
+        *reinterpret_cast<uint2*>(drow + nt * 256 + wv * 64 + g * 16 + 4 * (lane >> 4)) =
+            uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
       }
     }
   }
@@ -1080,6 +1111,10 @@ __device__ __forceinline__ void gemm_tile_i8(uint8_t* smem, const GemmLoads<Gemm
   // those of the chunks issued after it, kGemmAJ + 4 each.
   constexpr int kAhead = kGemmNA - 1;
   constexpr int kPer = kGemmAJ + kGemmBJ;
+  static_assert(RW <= 64, "one row scale per lane");
+  // the rows' scales, requested before the chunks (lane r holds row r's; the
+  // epilogue shuffles them out), so the epilogue does not wait a round trip
+  const float hsv = lane < rows ? hs[row0 + lane] : 0.0f;
 #pragma unroll
   for (int c = 0; c < kAhead + 1; ++c)
     if (c < KC) issue(c);
@@ -1103,10 +1138,12 @@ __device__ __forceinline__ void gemm_tile_i8(uint8_t* smem, const GemmLoads<Gemm
       const int r = mi * 16 + (lane & 15);
       const int32x4 p1 = *reinterpret_cast<const int32x4*>(As + a_swz(r, lane >> 4));
       const int32x4 p2 = *reinterpret_cast<const int32x4*>(As + a_swz(r, 4 + (lane >> 4)));
+      // weights as the first operand: the accumulator tile is the output
+      // transposed, so a lane holds four consecutive columns of one row
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        a1c[mi][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p1, q[g], a1c[mi][g], 0, 0, 0);
-        a2c[mi][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(p2, q[g], a2c[mi][g], 0, 0, 0);
+        a1c[mi][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(q[g], p1, a1c[mi][g], 0, 0, 0);
+        a2c[mi][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(q[g], p2, a2c[mi][g], 0, 0, 0);
       }
     }
     if (c + 1 < KC) {
@@ -1118,20 +1155,31 @@ __device__ __forceinline__ void gemm_tile_i8(uint8_t* smem, const GemmLoads<Gemm
         vm_barrier<0>();
     }
   }
-  // epilogue: lane holds rows 4*(lane/16)+j of each 16x16 tile, column lane%16
+  // epilogue: lane holds row mi*16 + lane%16 and columns 4*(lane/16) + j of
+  // cell g, stored as one 8-byte run. The column scales move to those lanes
+  // (lane c holds column c's) and the row scales likewise, with every lane
+  // taking part in the shuffles (an exec-masked source lane gives no data)
+  // before the lanes past the tile's rows drop out.
+  float scq[4][4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) scq[g][j] = __shfl(gl.sc[g], 4 * (lane >> 4) + j, 64);
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi) {
+    const int row = mi * 16 + (lane & 15);
+    const float rs = __shfl(hsv, row, 64);
+    if (row >= rows) continue;
+    uint16_t* drow = dst + (size_t)(row0 + row) * Ndim + nt * 256 + wv * 64 + 4 * (lane >> 4);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = mi * 16 + 4 * (lane >> 4) + j;
-      if (row >= rows) continue;
-      const float rs = hs[row0 + row];
-      uint16_t* drow = dst + (size_t)(row0 + row) * Ndim;
+    for (int g = 0; g < 4; ++g) {
+      float o[4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int j = 0; j < 4; ++j) {
         const float v = __fadd_rn(__fmul_rn((float)a1c[mi][g][j], 256.0f), (float)a2c[mi][g][j]);
-        drow[nt * 256 + wv * 64 + g * 16 + (lane & 15)] = f32_to_bf16_bits(__fmul_rn(__fmul_rn(v, rs), gl.sc[g]));
+        o[j] = __fmul_rn(__fmul_rn(v, rs), scq[g][j]);
       }
+      *reinterpret_cast<uint2*>(drow + g * 16) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
     }
   }
 }
@@ -1152,11 +1200,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   __shared__ __attribute__((aligned(1024))) uint8_t smem[Sh::kLds];
   // set-up scratch inside the ring (no loads are in flight yet)
   int* const mtp = reinterpret_cast<int*>(smem);
-  int* const tok = mtp + kMaxExperts + 1;
-  int* const wsum = tok + RW;
+  int* const offs = mtp + kMaxExperts + 1;
+  int* const wsum = offs + kMaxExperts + 1;
+  int* const tok = wsum + 4;
   const int tid = threadIdx.x, lane = tid & 63;
   const int NT = GATEUP ? I / 128 : D / 256;
-  tile_prefix<RW>(offsets, E, cap, mtp, wsum);
+  tile_prefix<RW>(offsets, E, cap, mtp, wsum, offs);
   const int ntiles = mtp[E] * NT;
   const int per = (ntiles + 7) >> 3;
   const int q = blockIdx.x >> 3;
@@ -1173,9 +1222,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
   // rows; every tile gets at least one row): tiles of one column block then run
   // at the same pace and meet each other's weight chunks in L2, where a full
   // tile and a nearly empty one would each fetch them
-  const int ne = min(offsets[e + 1] - offsets[e], cap);
+  const int ne = min(offs[e + 1] - offs[e], cap);
   const int tr = (((ne + nmt_e - 1) / nmt_e) + 15) & ~15;
-  const int row0 = __builtin_amdgcn_readfirstlane(offsets[e] + mt * tr);
+  const int row0 = __builtin_amdgcn_readfirstlane(offs[e] + mt * tr);
   const int rows = __builtin_amdgcn_readfirstlane(min(tr, ne - mt * tr));
   if (tid < RW) tok[tid] = (tid < rows) ? (GATEUP ? sorted_token[row0 + tid] : row0 + tid) : -1;
   __syncthreads();
@@ -1206,10 +1255,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(int D, int I, int E, const uint
       gl.sc[g] = chain_scale<CH>(sp[dg * 16 + (lane & 15)]);
     }
   }
-  // consume the scale loads here, so the compiler's waits for them sit before
-  // the chunk loop (inside it they would also drain the ring's loads); and no
-  // wave may start loading into the ring while another still reads tok
-  asm volatile("" ::"v"(gl.sc[0]), "v"(gl.sc[1]), "v"(gl.sc[2]), "v"(gl.sc[3]));
+  // kChainAct dequantises with the scales in the chunk loop: consume the scale
+  // loads here, so the compiler's waits for them sit before the loop (inside
+  // it they would also drain the ring's loads). kChainF32 applies them in the
+  // epilogue only, where the loads have long landed: leaving them in flight
+  // takes a global round trip off every tile's start. And no wave may start
+  // loading into the ring while another still reads tok.
+  if constexpr (CH != kChainF32) asm volatile("" ::"v"(gl.sc[0]), "v"(gl.sc[1]), "v"(gl.sc[2]), "v"(gl.sc[3]));
   __syncthreads();
   constexpr int PL = !GATEUP && CH == kChainF32 && !I8 ? 2 : 1;  // h planes of the down product
   if constexpr (I8) {
