@@ -595,6 +595,9 @@ __global__ __launch_bounds__(64 * TB) void k_route_mfma(int T, int D, int E, int
   const int lgp_floats = TB * 256 > 16 * E ? TB * 256 : 16 * E;
   int32_t* cand = reinterpret_cast<int32_t*>(lgp + lgp_floats) + w * E;
   float* cval = reinterpret_cast<float*>(reinterpret_cast<int32_t*>(lgp + lgp_floats) + TB * E) + w * E;
+  // the router columns' partial sums of squares, [D / 256][E], staged with the token rows
+  const int NPD = (D + 255) >> 8;
+  float* npl = reinterpret_cast<float*>(lds8 + TB * XRS) + lgp_floats + 2 * TB * E;
 
   // ---- phase 1 assignment: tiles tile0, tile0 + tstep, ... over steps [s0, s1) ----
   // Step st, k-lane kq takes the 8 hidden indices of piece p = 4 st + kq, with
@@ -616,15 +619,13 @@ __global__ __launch_bounds__(64 * TB) void k_route_mfma(int T, int D, int E, int
     const int p = 4 * st + kq;
     return *reinterpret_cast<const uint4*>(rtq + ((int64_t)((16 * tile + m) * 8 + (p >> LP)) * P + (p & (P - 1))) * 8);
   };
-  // the first batch of router fragments is requested before the token rows
-  uint4 b[8];
-  const bool pre = tile0 < NT && s1 - s0 >= 8;
-  if (pre) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) b[j] = bload(tile0, s0 + j);
-  }
+  // router fragments in batches of kRouteBatch steps per wave
+  constexpr int kRouteBatch = 8;
+  uint4 b[kRouteBatch];
+  const bool pre = tile0 < NT && s1 - s0 >= kRouteBatch;
 
-  // ---- the token rows into LDS (rows past T as zeros) ----
+  // ---- the token rows into LDS (rows past T as zeros), the norm partials,
+  // and the first batch of router fragments requested behind them ----
   {
     const int cpr = D >> 3;  // 16-byte pieces per row
     const int per = (TB * cpr) / (64 * TB);  // per thread (D / 512, exact)
@@ -638,6 +639,11 @@ __global__ __launch_bounds__(64 * TB) void k_route_mfma(int T, int D, int E, int
         v[k] = t0 + r < T ? reinterpret_cast<const uint4*>(x + (int64_t)(t0 + r) * D)[c] : uint4{0u, 0u, 0u, 0u};
       }
     }
+    if (pre) {
+#pragma unroll
+      for (int j = 0; j < kRouteBatch; ++j) b[j] = bload(tile0, s0 + j);
+    }
+    for (int i = threadIdx.x; i < NPD * E; i += 64 * TB) npl[i] = npart[i];
 #pragma unroll
     for (int k = 0; k < PMAX; ++k) {
       if (k < per) {
@@ -672,15 +678,15 @@ __global__ __launch_bounds__(64 * TB) void k_route_mfma(int T, int D, int E, int
         }
       };
       int st = s0;
-      bool have = tile == tile0 && pre;  // b holds steps s0 .. s0 + 7
-      for (; st + 8 <= s1; st += 8) {
+      bool have = tile == tile0 && pre;  // b holds steps s0 .. s0 + kRouteBatch - 1
+      for (; st + kRouteBatch <= s1; st += kRouteBatch) {
         if (!have) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) b[j] = bload(tile, st + j);
+          for (int j = 0; j < kRouteBatch; ++j) b[j] = bload(tile, st + j);
         }
         have = false;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) step(st + j, b[j]);
+        for (int j = 0; j < kRouteBatch; ++j) step(st + j, b[j]);
       }
       for (; st < s1; ++st) step(st, bload(tile, st));
 #pragma unroll
@@ -705,7 +711,6 @@ __global__ __launch_bounds__(64 * TB) void k_route_mfma(int T, int D, int E, int
   float ss = 0.0f;
   for (int k2 = 0; k2 < KS; ++k2) ss += nxp[k2][w];
   const float nxv = sqrtf(ss);
-  const int NPD = (D + 255) >> 8;
   float lo[EPL], hi[EPL];
   bool bad = !(nxv <= 3.0e38f);
 #pragma unroll
@@ -717,7 +722,7 @@ __global__ __launch_bounds__(64 * TB) void k_route_mfma(int T, int D, int E, int
       float v = lgp[w * E + e];
       for (int k2 = 1; k2 < KS; ++k2) v += lgp[(k2 * 16 + w) * E + e];
       float n2 = 0.0f;
-      for (int p = 0; p < NPD; ++p) n2 += npart[(int64_t)p * E + e];
+      for (int p = 0; p < NPD; ++p) n2 += npl[p * E + e];
       const float dl = __builtin_fmaf(cbound * nxv, sqrtf(n2), 1e-30f);
       lo[i] = v - dl;
       hi[i] = v + dl;
@@ -1115,7 +1120,7 @@ static void launch_route_mfma_k(const kmoe_desc& d, const uint16_t* x, const uin
   const int T = (int)d.tokens, D = (int)d.hidden, E = (int)d.num_experts, K = (int)d.top_k;
   const int XRS = (D / 64) * kRouteSliceBytes + 16;
   const int lgp = TB * 256 > 16 * E ? TB * 256 : 16 * E;
-  const size_t lds = (size_t)TB * XRS + 4 * ((size_t)lgp + 2 * (size_t)TB * E);
+  const size_t lds = (size_t)TB * XRS + 4 * ((size_t)lgp + 2 * (size_t)TB * E + (size_t)((D + 255) / 256) * E);
   hipLaunchKernelGGL((k_route_mfma<EPL, P, TB>), dim3((T + TB - 1) / TB), dim3(64 * TB), lds, st, T, D, E, K, x, rtq,
                      npart, cb, topk_idx, topk_w, hist, d.act_dtype == KMOE_DTYPE_BF16 ? 1 : 0);
 }
