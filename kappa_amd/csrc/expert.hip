@@ -1339,7 +1339,9 @@ __global__ __launch_bounds__(256) void k_h_planes(int M, int I, uint16_t* __rest
   // each bf16 plane, 8-byte stores of each int8 plane)
   constexpr int kSteps = kPlanesMaxChunks / 8;
   float v[kSteps][8];
-  float mx = 0.0f;
+  // the largest |h| as f32 bits: above 0x7f7fffff for an inf or a NaN (which
+  // fmaxf would pass over)
+  uint32_t mb = 0;
 #pragma unroll
   for (int st = 0; st < kSteps; ++st) {
     const int e = 8 * (lane + 64 * st);
@@ -1353,15 +1355,13 @@ __global__ __launch_bounds__(256) void k_h_planes(int M, int I, uint16_t* __rest
         v[st][2 * i + 1] = __uint_as_float(hw[i] & 0xffff0000u) + __uint_as_float(lw[i] & 0xffff0000u);
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[st][i]));
+      for (int i = 0; i < 8; ++i) mb = max(mb, __float_as_uint(v[st][i]) & 0x7fffffffu);
     }
   }
-  bool bad = !(mx <= 3.4e38f);
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-    bad = bad || __shfl_xor((int)bad, o, 64);
-  }
+  for (int o = 32; o >= 1; o >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, o, 64));
+  const bool bad = mb > 0x7f7fffffu;
+  const float mx = __uint_as_float(mb);
   int k = 0;
   if (!bad && mx > 0.0f) {
     int ex;

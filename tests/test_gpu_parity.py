@@ -477,6 +477,38 @@ def test_large_chunk_nonfinite_row_stays_in_its_token(dev, l30):
     assert mean_rel(outs[0][keep], outs[1][keep]) <= 1e-5
 
 
+@pytest.mark.parametrize("T", [8, 64, 512, 2048])
+def test_nan_gate_scale_reaches_exactly_its_experts_tokens(dev, l30, T):
+    """A NaN scale on one gate column of expert e: in the reference every h row
+    of e is NaN in that column (silu(g) * u, kappa/qwen3/ffn_moe.py:209), so
+    y = h @ W_down is NaN across the row and so is the output of every token
+    routed to e, with no inf anywhere; every other token's output is unchanged
+    (bit-identical to the clean layer). T = 8 and 64 run the decode kernels,
+    512 the hi + lo down GEMM, 2048 the int8-plane down product, whose plane
+    pass must flag a row holding a NaN and no inf."""
+    from kappa_amd.qwen3 import Q8Weight
+    from kappa_amd.qwen3.ffn_moe import _moe_forward
+
+    x = make_x(T, l30.D, seed=1900 + T)
+    r, _ = _route_and_dispatch(x, l30.router, l30.E, l30.K)
+    idx = r["idx"].cpu().numpy()
+    e = int(idx[0, 0])
+    sc = l30.gate.scale.clone()
+    sc[e, 0, 5] = float("nan")
+    gates = (Q8Weight(l30.gate.values, sc), l30.gate)
+    outs = []
+    for g in gates:
+        o = _moe_forward(
+            x.reshape(1, T, l30.D), l30.router, g, l30.up, l30.down, num_experts=l30.E,
+            num_experts_per_tok=l30.K, packed=None, **forward_args("ragged"),
+        )  # fmt: skip
+        outs.append(bf16_np(o.reshape(T, l30.D)))
+    hit = (idx == e).any(axis=1)
+    print(f"T={T}: expert {e} holds {int(hit.sum())} tokens")
+    assert np.isnan(outs[0][hit]).all()
+    assert np.array_equal(outs[0][~hit], outs[1][~hit])
+
+
 @pytest.mark.parametrize("T", [4, 64, 512])
 def test_packed_experts_alone(dev, l30, T):
     """A model that prepacked at load time passes packed= and no source weights; the
