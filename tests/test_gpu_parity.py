@@ -266,15 +266,17 @@ def _prefill_sampled(layer, T, seed, router=None, x=None, n_tok=48, impl="ragged
     return od
 
 
-@pytest.mark.parametrize("T", [240, 512, 704, 1024, 1280, 1535, 1536, 2048, 4096])
+@pytest.mark.parametrize("T", [240, 512, 704, 1024, 1280, 1535, 1536, 2048, 2049, 3001, 4096])
 def test_30b_prefill_ragged(dev, l30, T):
     """The prefill chunks under the reference's ragged program (ragged_jax with its
     default threshold of 64: these sizes run _moe_ragged). Every grouped-GEMM tile
     form is reached: 64-row tiles (T=240, 512, 704), 128-row tiles with
     nontemporal weights (T=1024, 64 rows per expert) and without (T=1280, 80),
-    160-row tiles with (T=2048) and without (T=4096). From T=1536 (96 rows per
-    expert) the down product takes h as int8 planes; T=1535 is the last size
-    with the bf16 hi and lo planes."""
+    160-row tiles with (T=2048) and without (T=3001, 4096). From T=1536 (96 rows
+    per expert) the down product takes h as int8 planes; T=1535 is the last size
+    with the bf16 hi and lo planes. T=2049 and 3001 leave the two-phase router
+    a last block of one and of nine tokens and the dispatch a partial 64-token
+    chunk."""
     from kappa_amd.qwen3 import moe_layer_config
 
     cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_impl="ragged_jax")
@@ -919,10 +921,11 @@ def test_two_phase_router_ties_near_ties_and_fallback(dev):
     assert np.isfinite(lg[1]).all()
 
 
-@pytest.mark.parametrize("T", [512, 2048, 4096])
+@pytest.mark.parametrize("T", [512, 2048, 2049, 3001, 4096])
 def test_forward_routing_two_phase(dev, l30, T):
     """kmoe_forward from 2048 tokens routes with the two-phase form (below, the
-    all-VALU router): its indices and weights equal the stage router's."""
+    all-VALU router): its indices and weights equal the stage router's, also
+    where its last block holds fewer than 16 tokens (T = 2049, 3001)."""
     from kappa_amd.qwen3 import moe_stages
     from kappa_amd.qwen3.ffn_moe import _moe_forward
 
