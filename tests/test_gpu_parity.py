@@ -323,6 +323,16 @@ def test_30b_skewed_routing(dev, l30):
             assert int(np.max(od["group_sizes"])) > 128
 
 
+@pytest.mark.parametrize("T", [512, 1000, 1536])
+def test_235b_prefill_tile_forms(dev, T):
+    """The 235B-A22B layer (D = 4096, I = 1536) on the grouped GEMMs' other
+    tile forms: 64-row tiles (T = 512, 32 rows per expert), 128-row tiles with
+    nontemporal weights (T = 1000, ~62 rows), and 160-row tiles with the down
+    product on int8 planes of h (T = 1536, 96 rows)."""
+    layer = make_layer("235b", seed=1)
+    _prefill_sampled(layer, T, seed=2300 + T, n_tok=16)
+
+
 def test_235b_layer(dev):
     from kappa_amd import _lib
     from kappa_amd.qwen3 import moe_block_ffn, moe_stages, moe_swiglu_ffn, rms_norm
