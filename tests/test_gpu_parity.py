@@ -283,6 +283,20 @@ def test_30b_prefill_ragged(dev, l30, T):
     _prefill_sampled(l30, T, seed=100 + T, cfg=cfg)
 
 
+@pytest.mark.parametrize("K", [1, 2, 4])
+def test_30b_other_top_k(dev, l30, K):
+    """The reference takes any num_experts_per_tok: the 30B-A3B layer with top-1,
+    top-2 and top-4 routing on the packed kernels of each size class (the
+    whole-block decode call with its fused down + combine at T = 1 and 4, the
+    decode kernels at T = 64, the grouped GEMMs at T = 1024 and 4096), under
+    the ragged program."""
+    import dataclasses
+
+    layer = dataclasses.replace(l30, K=K)
+    for T in (1, 4, 64, 1024, 4096):
+        _prefill_sampled(layer, T, seed=2600 + 10 * K + T, n_tok=16)
+
+
 @pytest.mark.parametrize("T", [512, 1024, 4096])
 def test_30b_prefill_gather_per_tensor(dev, l30t, T):
     """The gather program (the default impl) at prefill sizes on the grouped GEMMs
