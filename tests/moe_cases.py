@@ -23,6 +23,11 @@ import torch
 SHAPES = {
     "30b": dict(D=2048, E=128, K=8, I=768),
     "235b": dict(D=4096, E=128, K=8, I=1536),
+    # shapes outside the Qwen3 presets (GPU tests only): load batches that do
+    # not divide a wave's chunks (D / 64 = 40, I / 64 = 16), 64 experts, top-6;
+    # and 256 experts
+    "odd": dict(D=2560, E=64, K=6, I=1024),
+    "e256": dict(D=2048, E=256, K=8, I=768),
 }
 
 

@@ -283,6 +283,19 @@ def test_30b_prefill_ragged(dev, l30, T):
     _prefill_sampled(l30, T, seed=100 + T, cfg=cfg)
 
 
+@pytest.mark.parametrize("shape", ["odd", "e256"])
+def test_other_layer_shapes(dev, shape):
+    """Layers outside the Qwen3 presets through every size class of the packed
+    kernels, against the oracle: D = 2560, I = 1024, E = 64, top-6 (the decode
+    GEMVs' guarded load batches, whose chunks a wave's batches do not divide;
+    the all-VALU router at every size, D / 64 = 40 slices padded to 64; the
+    int8-plane down product at T = 2048, 192 rows per expert), and 256 experts
+    (D = 2048, I = 768, top-8)."""
+    layer = make_layer(shape, seed=3)
+    for T in (1, 4, 8, 40, 64, 200, 1000, 2048):
+        _prefill_sampled(layer, T, seed=2700 + T, n_tok=12)
+
+
 @pytest.mark.parametrize("K", [1, 2, 4])
 def test_30b_other_top_k(dev, l30, K):
     """The reference takes any num_experts_per_tok: the 30B-A3B layer with top-1,
