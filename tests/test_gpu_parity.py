@@ -296,6 +296,14 @@ def test_other_layer_shapes(dev, shape):
         _prefill_sampled(layer, T, seed=2700 + T, n_tok=12)
 
 
+def test_other_layer_shape_gather_per_tensor(dev):
+    """The D = 2560, I = 1024, 64-expert, top-6 layer with per-tensor W8 under
+    the gather program (the x.dtype chain of the same kernels)."""
+    layer = make_layer("odd", seed=4, per_tensor=True)
+    for T in (1, 8, 64, 1000):
+        _prefill_sampled(layer, T, seed=2800 + T, n_tok=12, impl="gather_einsum")
+
+
 @pytest.mark.parametrize("K", [1, 2, 4])
 def test_30b_other_top_k(dev, l30, K):
     """The reference takes any num_experts_per_tok: the 30B-A3B layer with top-1,
