@@ -44,7 +44,7 @@ def check_out(out: np.ndarray, ref: np.ndarray, bf16: bool, what: str = "out"):
 
 @pytest.mark.parametrize("act", ["bf16", "f32"])
 @pytest.mark.parametrize("scale_dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("D", [16, 100, 192, 2048, 4096])
+@pytest.mark.parametrize("D", [16, 100, 192, 2048, 2560, 4096])
 def test_rms_norm_bit_exact(dev, act, scale_dtype, D):
     from kappa_amd.qwen3 import rms_norm
 
@@ -116,6 +116,25 @@ def test_30b_fused_block_equals_separate_calls(dev, l30, T):
         fused = moe_block_ffn(h, sc, l30.router, l30.gate, l30.up, l30.down, cfg=cfg)
         assert fused.dtype == h.dtype and fused.shape == h.shape
         assert torch.equal(fused, composed)
+
+
+@pytest.mark.parametrize("T", [8, 100, 241])
+def test_other_shape_fused_block_equals_separate_calls(dev, T):
+    """The block call on a layer outside the Qwen3 presets (D = 2560: 40 router
+    slices, the split router normalising its rows at T <= 240, the norm kernel
+    above), bit for bit against its composition."""
+    from kappa_amd.qwen3 import moe_block_ffn, moe_swiglu_ffn, rms_norm
+
+    layer = make_layer("odd", seed=5)
+    cfg = layer_cfg(layer, "ragged")
+    h = make_x(T, layer.D, seed=950 + T).reshape(1, T, layer.D) * 4.0
+    sc = _norm_scale(layer.D, T, dev)
+    h2 = rms_norm(h, sc)
+    want_h2 = oracle.rms_norm(bf16_np(h.reshape(T, layer.D)), sc.float().cpu().numpy(), 1e-6, True)
+    np.testing.assert_array_equal(bf16_np(h2.reshape(T, layer.D)), want_h2)
+    composed = h + moe_swiglu_ffn(h2, layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
+    fused = moe_block_ffn(h, sc, layer.router, layer.gate, layer.up, layer.down, cfg=cfg)
+    assert torch.equal(fused, composed)
 
 
 def test_30b_fused_block_fixed_capacity(dev, l30):
