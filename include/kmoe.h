@@ -230,7 +230,7 @@ kmoe_status kmoe_route(const kmoe_desc* desc, const void* x, const kmoe_weight* 
                        void* scratch, size_t scratch_bytes, int32_t* topk_idx, float* topk_w, int32_t* block_hist,
                        void* stream);
 /* Bytes of scratch the two-phase form of kmoe_route needs (the router
- * transposed to f32 and its column norms). */
+ * transposed to bf16 and its column norms' partial sums). */
 kmoe_status kmoe_route_scratch_bytes(const kmoe_desc* desc, size_t* bytes);
 
 /* Stable sort of assignments by expert (kappa/qwen3/ffn_moe.py:189-200, 212):
