@@ -224,7 +224,7 @@ kmoe_status kmoe_rms_norm(const kmoe_desc* desc, const void* x, const void* scal
  * two-phase form when x and the router are bf16, D is 512, 1024, 2048 or
  * 4096, E % 16 == 0 and E <= 256: every logit on the matrix cores, then the
  * canonical order only for the experts within a rigorous f32 error bound of the
- * K-th (the form kmoe_forward uses above 240 tokens). Selections, weights and
+ * K-th (the form kmoe_forward uses from 2048 tokens). Selections, weights and
  * block_hist are the same either way. */
 kmoe_status kmoe_route(const kmoe_desc* desc, const void* x, const kmoe_weight* router, float* logits,
                        void* scratch, size_t scratch_bytes, int32_t* topk_idx, float* topk_w, int32_t* block_hist,
