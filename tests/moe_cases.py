@@ -28,6 +28,9 @@ SHAPES = {
     # and 256 experts
     "odd": dict(D=2560, E=64, K=6, I=1024),
     "e256": dict(D=2048, E=256, K=8, I=768),
+    # I not a multiple of 128 (fifteen 64-wide chunks): the grouped GEMM for
+    # such shapes (k_prefill) and decode GEMVs whose waves take unequal chunks
+    "i960": dict(D=2048, E=32, K=4, I=960),
 }
 
 

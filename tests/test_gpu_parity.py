@@ -283,14 +283,16 @@ def test_30b_prefill_ragged(dev, l30, T):
     _prefill_sampled(l30, T, seed=100 + T, cfg=cfg)
 
 
-@pytest.mark.parametrize("shape", ["odd", "e256"])
+@pytest.mark.parametrize("shape", ["odd", "e256", "i960"])
 def test_other_layer_shapes(dev, shape):
     """Layers outside the Qwen3 presets through every size class of the packed
     kernels, against the oracle: D = 2560, I = 1024, E = 64, top-6 (the decode
     GEMVs' guarded load batches, whose chunks a wave's batches do not divide;
     the all-VALU router at every size, D / 64 = 40 slices padded to 64; the
-    int8-plane down product at T = 2048, 192 rows per expert), and 256 experts
-    (D = 2048, I = 768, top-8)."""
+    int8-plane down product at T = 2048, 192 rows per expert); 256 experts
+    (D = 2048, I = 768, top-8); and I = 960 with 32 experts, top-4 (fifteen
+    64-wide chunks: the grouped GEMM for I % 128 != 0, unequal chunk counts
+    per wave in the decode down GEMV and the fused down + combine)."""
     layer = make_layer(shape, seed=3)
     for T in (1, 4, 8, 40, 64, 200, 1000, 2048):
         _prefill_sampled(layer, T, seed=2700 + T, n_tok=12)
