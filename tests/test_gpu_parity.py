@@ -320,6 +320,18 @@ def test_30b_other_top_k(dev, l30, K):
         _prefill_sampled(layer, T, seed=2600 + 10 * K + T, n_tok=16)
 
 
+@pytest.mark.parametrize("T", [8192, 16384, 32768])
+def test_30b_prefill_whole_prompts(dev, l30, T):
+    """Prefill without chunking (the reference's default, prefill_chunk_size=None,
+    kappa/qwen3/generate.py:48-65, passes a whole prompt to the layer): up to
+    32768 tokens (262144 assignment rows, ~2000 rows per expert) under the
+    ragged program, routing in full and sampled rows against the oracle."""
+    from kappa_amd.qwen3 import moe_layer_config
+
+    cfg = moe_layer_config(hidden=l30.D, experts=l30.E, top_k=l30.K, intermediate=l30.I, moe_impl="ragged_jax")
+    _prefill_sampled(l30, T, seed=3000 + T, cfg=cfg, n_tok=16)
+
+
 @pytest.mark.parametrize("T", [512, 1024, 4096])
 def test_30b_prefill_gather_per_tensor(dev, l30t, T):
     """The gather program (the default impl) at prefill sizes on the grouped GEMMs
